@@ -1,0 +1,184 @@
+"""compress-zip on one MI355X: compress tokens/s at L4 (512-token chunks).
+
+One step = the whole workload compressed on the device: every chunk goes
+through the batched causal prefill (int8 MFMA GEMMs, exact attention), the
+fused logits -> CDF stage and the arithmetic coder, with the tokens already
+resident in HBM.  Prints one JSON line (see the repository's bench contract).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "compress-zip_amd"))
+
+import numpy as np  # noqa: E402
+
+# MI355X published peaks (dense)
+PEAK_INT8_TOPS = 5000.0     # TOP/s
+PEAK_HBM_GBS = 8000.0       # GB/s
+
+WORKLOADS = {
+    # shipped model, level 4 (512-token chunks), 64 MiB of seeded synthetic text
+    "v001_L4_ctx512_text64MiB": dict(model="shipped", chunk=512, text_bytes=64 << 20),
+    # shipped model, level 4, Zipf(1.1) token ids (no tokenizer step)
+    "v001_L4_ctx512_zipf16M": dict(model="shipped", chunk=512, ids=16 << 20),
+}
+DEFAULT = "v001_L4_ctx512_zipf16M"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_tokens(wl, model_path, vocab):
+    from czip_amd import synth
+    if "ids" in wl:
+        return synth.zipf_ids(wl["ids"], vocab, seed=7)
+    raise SystemExit("text workloads need the tokenizer (not built yet)")
+
+
+def gemm_ops_per_token(cfg, kv_mode):
+    d, F, V, G = cfg["d_model"], cfg["d_ff"], cfg["vocab_size"], cfg["n_kv_heads"]
+    qkv_n = d + 2 * G * 64 if kv_mode == 1 else d + 128
+    per_layer = {"gemm_qkv": qkv_n * d, "gemm_o": d * d, "gemm_up": 2 * F * d, "gemm_down": d * F}
+    out = {k: 2 * v * cfg["n_layers"] for k, v in per_layer.items()}
+    out["gemm_head"] = 2 * V * d
+    return out
+
+
+def cpu_baseline(model_path, tokens, chunk, budget_s=15.0):
+    """Oracle (C restatement of the Rust chunk loop) on the host cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    try:
+        lib_path = oracle.build(native=True)
+        kind_note = "gcc -O3 -march=native"
+    except Exception:
+        lib_path = oracle.LIB_PATH
+        kind_note = "gcc -O3 -march=x86-64-v3"
+    L = oracle.load(lib_path)
+    m = oracle.Model.from_file(model_path, lib_handle=L)
+    cores = min(16, len(os.sched_getaffinity(0)))
+    nchunks = len(tokens) // chunk
+    # calibrate with one chunk per thread, then size the sample to the budget
+    k0 = min(nchunks, cores)
+    t = time.perf_counter()
+    m.compress_many(tokens[:k0 * chunk], chunk, threads=cores)
+    dt0 = time.perf_counter() - t
+    per_round = max(dt0, 1e-3)
+    rounds = max(1, int(budget_s / per_round))
+    k = min(nchunks, cores * rounds)
+    t = time.perf_counter()
+    m.compress_many(tokens[:k * chunk], chunk, threads=cores)
+    dt = time.perf_counter() - t
+    return {"value": round(k * chunk / dt, 1), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"first {k} chunks x {chunk} tokens ({k * chunk} tokens) of the same workload, "
+                      f"{cores} threads, C oracle ({kind_note}), {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); chunks shard across GPUs with no "
+              f"communication, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+    import czip_amd
+    if not os.path.exists(czip_amd.LIB_PATH):
+        from czip_amd import build as b
+        b.build()
+    wl = WORKLOADS[args.workload]
+    model_path = os.path.join(ROOT, "models", "v001_eng.czm")
+    kv_mode = czip_amd.KV_RUST_COMPAT
+    weights = czip_amd.ModelWeights(model_path, kv_mode)
+    cfg = weights.config
+    tokens = make_tokens(wl, model_path, cfg["vocab_size"])
+    chunk = wl["chunk"]
+    n = int(tokens.size)
+    log(f"workload {args.workload}: {n} tokens, chunk {chunk}")
+    model = czip_amd.Model(weights, device=0)
+    job = model.compress_plan(tokens, chunk)
+    for _ in range(args.warmup):
+        job.run()
+    model.reset_stats()
+    model.set_profiling(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        job.run()
+    t1 = time.perf_counter()
+    model.set_profiling(False)
+    ms = (t1 - t0) * 1000.0 / args.steps
+    chunks = job.fetch()
+    job.free()
+    coded = sum(len(c) for c in chunks)
+    value = n / (ms / 1000.0)
+
+    # per-kernel breakdown from HIP events on the context stream
+    ops = gemm_ops_per_token(cfg, kv_mode)
+    nrows = ((n + chunk - 1) // chunk) * chunk
+    kernels = {}
+    for name in ["prep", "embed_norm", "gemm_qkv", "attention", "gemm_o", "row_norm", "gemm_up", "gemm_down",
+                 "gemm_head", "cdf", "encode"]:
+        launches, tot = model.kernel_stats(name)
+        if launches:
+            kernels[name] = {"launches": launches, "avg_ms": tot / launches, "ms_per_step": tot / args.steps}
+    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
+    gemm_ms = sum(kernels[k]["ms_per_step"] for k in kernels if k.startswith("gemm"))
+    gemm_tops = sum(ops.values()) * nrows / (gemm_ms / 1000.0) / 1e12 if gemm_ms else 0.0
+    if dom.startswith("gemm"):
+        per_launch = ops[dom] * nrows / (kernels[dom]["launches"] / args.steps)
+        ach = per_launch / (kernels[dom]["avg_ms"] / 1000.0) / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": None, "kernel": dom}
+    elif dom == "attention":
+        H, T = cfg["n_heads"], chunk
+        flops_per_chunk = sum(2 * 2 * H * 64 * (p + 1) for p in range(T)) * cfg["n_layers"]
+        per_launch = flops_per_chunk * (nrows // T) / (kernels[dom]["launches"] / args.steps)
+        ach = per_launch / (kernels[dom]["avg_ms"] / 1000.0) / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                "frac": round(ach / PEAK_INT8_TOPS, 5), "traffic": None, "kernel": dom}
+    else:
+        V = cfg["vocab_size"]
+        per_launch = (4 * V + 8) * nrows / (kernels[dom]["launches"] / args.steps)
+        ach = per_launch / (kernels[dom]["avg_ms"] / 1000.0) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "kernel": dom}
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(model_path, tokens, chunk, args.cpu_budget)
+    line = {
+        "metric": "compress tok/s (bit-exact .czip payload) at L4 ctx512, 1 GPU",
+        "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": args.workload, "model": "v001_eng.czm", "chunk_tokens": chunk, "tokens": n,
+                   "chunks": len(chunks), "kv_mode": "rust_compat", "parallelism": "chunks"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "gemm_int8_tops": round(gemm_tops, 2),
+        "coded_bytes": coded,
+        "kernels": {k: {"avg_ms": round(v["avg_ms"], 4), "ms_per_step": round(v["ms_per_step"], 3),
+                        "launches_per_step": v["launches"] // args.steps} for k, v in kernels.items()},
+    }
+    if cpu:
+        line["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,602 @@
+// C-ABI implementation of libczip_hip: model loading, device context,
+// batched prefill / CDF / coding jobs.  See include/czip_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "czip_internal.h"
+#include "czip_kernels.h"
+
+using namespace czip;
+
+namespace {
+
+constexpr uint32_t BOS = 1022u;  // main.rs:222, 387
+
+struct DevLayer {
+    int8_t *attn_norm = nullptr, *post_attn_norm = nullptr, *ffn_norm = nullptr, *post_ffn_norm = nullptr;
+    int8_t *qkv_w = nullptr, *out_w = nullptr, *up_w = nullptr, *down_w = nullptr, *sink = nullptr;
+    int32_t* score_mult = nullptr;
+    int qkv_mult, out_mult, up_mult, down_mult, qkv_shift, out_shift, up_shift, down_shift;
+    int qkv_n;  // QKV rows the attention reads
+};
+
+struct Stat {
+    int64_t launches = 0;
+    double ms = 0;
+};
+
+}  // namespace
+
+struct czip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    czip_model_desc cfg{};
+    int KH = 1;  // cached KV heads per layer
+    std::vector<void*> allocs;
+    int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr;
+    uint16_t* lut = nullptr;
+    int16_t *rcos = nullptr, *rsin = nullptr;
+    std::vector<DevLayer> layers;
+    std::string err;
+    bool profiling = false;
+    std::map<std::string, Stat> stats;
+    struct Pending {
+        std::string name;
+        hipEvent_t a, b;
+    };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> event_pool;
+};
+
+struct czip_job {
+    czip_ctx* ctx = nullptr;
+    int kind = 0;  // 0 compress
+    int64_t n_tokens = 0, nchunks = 0;
+    int T = 0, BC = 0;
+    int64_t slot = 0;
+    std::vector<void*> allocs;
+    uint32_t* tok = nullptr;
+    uint8_t* out = nullptr;
+    int32_t* out_lens = nullptr;
+    int32_t* err = nullptr;
+    // per sub-batch scratch
+    uint32_t *inp = nullptr, *tgt = nullptr, *lohi = nullptr;
+    int32_t* lens = nullptr;
+    int32_t* x = nullptr;
+    int8_t *xn = nullptr, *q8 = nullptr, *kc = nullptr, *vc = nullptr, *attn = nullptr, *y8 = nullptr, *r8 = nullptr;
+    int32_t* logits = nullptr;
+};
+
+namespace {
+
+czip_status fail(czip_ctx* c, czip_status rc, const std::string& msg) {
+    if (c) c->err = msg;
+    return rc;
+}
+
+#define HIPCHECK(ctx, call)                                                                   \
+    do {                                                                                      \
+        hipError_t e_ = (call);                                                               \
+        if (e_ != hipSuccess)                                                                 \
+            return fail((ctx), CZIP_E_HIP, std::string(#call) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+template <typename T>
+czip_status dalloc(czip_ctx* c, std::vector<void*>& owner, T** p, size_t count) {
+    void* q = nullptr;
+    size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+    bytes = (bytes + 255) & ~(size_t)255;
+    hipError_t e = hipMalloc(&q, bytes);
+    if (e != hipSuccess) return fail(c, CZIP_E_NOMEM, std::string("hipMalloc(") + std::to_string(bytes) + "): " + hipGetErrorString(e));
+    owner.push_back(q);
+    *p = (T*)q;
+    return CZIP_OK;
+}
+
+template <typename T>
+czip_status upload(czip_ctx* c, T** dst, const T* src, size_t count) {
+    czip_status rc = dalloc(c, c->allocs, dst, count);
+    if (rc) return rc;
+    HIPCHECK(c, hipMemcpy(*dst, src, count * sizeof(T), hipMemcpyHostToDevice));
+    return CZIP_OK;
+}
+
+// --- launch instrumentation ---
+hipEvent_t take_event(czip_ctx* c) {
+    if (!c->event_pool.empty()) {
+        hipEvent_t e = c->event_pool.back();
+        c->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+struct Timed {
+    czip_ctx* c;
+    const char* name;
+    hipEvent_t a = nullptr, b = nullptr;
+    Timed(czip_ctx* c_, const char* n) : c(c_), name(n) {
+        if (c->profiling) {
+            a = take_event(c);
+            b = take_event(c);
+            if (a) hipEventRecord(a, c->stream);
+        }
+    }
+    ~Timed() {
+        if (c->profiling && a && b) {
+            hipEventRecord(b, c->stream);
+            c->pending.push_back({name, a, b});
+        }
+    }
+};
+
+void resolve_events(czip_ctx* c) {
+    for (auto& p : c->pending) {
+        float ms = 0;
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            auto& s = c->stats[p.name];
+            s.launches++;
+            s.ms += ms;
+        }
+        c->event_pool.push_back(p.a);
+        c->event_pool.push_back(p.b);
+    }
+    c->pending.clear();
+}
+
+czip_status check_config(czip_ctx* c, const czip_model_desc& w) {
+    if (w.head_dim != 64) return fail(c, CZIP_E_CONFIG, "head_dim must be 64 (attention.rs:9)");
+    if (w.n_heads < 1 || w.d_model != w.n_heads * 64) return fail(c, CZIP_E_CONFIG, "d_model must equal n_heads*64");
+    if (w.d_model > 1024) return fail(c, CZIP_E_CONFIG, "d_model > 1024 unsupported");
+    if (w.d_ff < 32 || w.d_ff % 32 != 0) return fail(c, CZIP_E_CONFIG, "d_ff must be a multiple of 32");
+    if (w.d_ff % 64 != 0) return fail(c, CZIP_E_CONFIG, "d_ff must be a multiple of 64");
+    if (w.vocab < 2 || w.vocab > 8192 || w.vocab % 64 != 0) return fail(c, CZIP_E_CONFIG, "vocab must be a multiple of 64 in [64, 8192]");
+    if (w.n_layers < 1) return fail(c, CZIP_E_CONFIG, "n_layers must be >= 1");
+    if (w.n_kv_heads < 1) return fail(c, CZIP_E_CONFIG, "n_kv_heads must be >= 1");
+    if (w.kv_mode == CZIP_KV_RUST_COMPAT) {
+        if (!(w.n_heads == 4 || w.n_heads == 6 || w.n_heads == 8))
+            return fail(c, CZIP_E_HEADS, "n_heads must be 4, 6 or 8 in rust-compat KV mode (attention.rs:172)");
+        int len = w.d_model + 2 * w.n_kv_heads * 64;
+        if (len / (w.d_model + 128) != 1) return fail(c, CZIP_E_HEADS, "QKV row splits into more than one MQA row (attention.rs:176)");
+    } else if (w.kv_mode == CZIP_KV_GQA) {
+        if (w.n_heads % w.n_kv_heads != 0) return fail(c, CZIP_E_CONFIG, "n_heads must be a multiple of n_kv_heads");
+    } else {
+        return fail(c, CZIP_E_ARG, "unknown kv_mode");
+    }
+    if (w.exp2_len != 256) return fail(c, CZIP_E_FORMAT, "Exp2 LUT must have exactly 256 entries (lut.rs:57-64)");
+    if (w.context_length < 1 || w.rope_len != (int64_t)w.context_length * 32)
+        return fail(c, CZIP_E_FORMAT, "RoPE LUT arrays size mismatch with max_seq_len * half_dim (lut.rs:148-165)");
+    if ((uint64_t)w.target_total <= (uint64_t)w.vocab) return fail(c, CZIP_E_CONFIG, "target_total must exceed vocab");
+    return CZIP_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+// Model loader
+// ===========================================================================
+extern "C" czip_status czip_model_load(const char* path, int32_t kv_mode, czip_model** out) {
+    if (!path || !out) return CZIP_E_ARG;
+    auto m = std::make_unique<czip_model>();
+    std::string err;
+    czip_status rc = load_czm(path, kv_mode, m->hm, err);
+    if (rc) {
+        fprintf(stderr, "czip_model_load: %s\n", err.c_str());
+        return rc;
+    }
+    *out = m.release();
+    return CZIP_OK;
+}
+
+extern "C" const czip_model_desc* czip_model_desc_get(const czip_model* m) { return m ? &m->hm.desc : nullptr; }
+
+extern "C" const uint8_t* czip_model_tokenizer(const czip_model* m, size_t* len, const char** codec) {
+    if (!m) return nullptr;
+    if (len) *len = m->hm.tokenizer_len;
+    if (codec) *codec = m->hm.tokenizer_codec.c_str();
+    return m->hm.tokenizer;
+}
+
+extern "C" void czip_model_free(czip_model* m) { delete m; }
+
+// ===========================================================================
+// Context
+// ===========================================================================
+extern "C" int czip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+extern "C" const char* czip_last_error(const czip_ctx* c) { return c ? c->err.c_str() : "null context"; }
+
+extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ctx** out) {
+    if (!w || !out) return CZIP_E_ARG;
+    *out = nullptr;
+    auto c = std::make_unique<czip_ctx>();
+    czip_status rc = check_config(c.get(), *w);
+    if (rc) {
+        fprintf(stderr, "czip_create: %s\n", c->err.c_str());
+        return rc;
+    }
+    c->cfg = *w;
+    c->cfg.layers = nullptr;
+    c->device = device;
+    if (hipSetDevice(device) != hipSuccess) return CZIP_E_HIP;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return CZIP_E_HIP;
+    const size_t d = (size_t)w->d_model, F = (size_t)w->d_ff, V = (size_t)w->vocab, G = (size_t)w->n_kv_heads;
+    c->KH = w->kv_mode == CZIP_KV_GQA ? w->n_kv_heads : 1;
+    czip_ctx* C = c.get();
+#define UP(dst, src, n) if ((rc = upload(C, &dst, src, n))) return rc;
+    UP(c->embed, w->embed, V * d)
+    UP(c->final_norm, w->final_norm, d)
+    UP(c->head_w, w->head_w, V * d)
+    UP(c->lut, w->exp2_lut, 256)
+    UP(c->rcos, w->rope_cos, (size_t)w->rope_len)
+    UP(c->rsin, w->rope_sin, (size_t)w->rope_len)
+    c->layers.resize((size_t)w->n_layers);
+    std::vector<int8_t> perm(2 * F * d);
+    for (int l = 0; l < w->n_layers; l++) {
+        const czip_layer_desc& L = w->layers[l];
+        DevLayer& D = c->layers[(size_t)l];
+        if (!L.attn_norm || !L.post_attn_norm || !L.ffn_norm || !L.post_ffn_norm || !L.qkv_w || !L.out_w || !L.up_w ||
+            !L.down_w || !L.score_mult)
+            return fail(C, CZIP_E_ARG, "layer tensor pointer is NULL");
+        D.qkv_n = w->kv_mode == CZIP_KV_GQA ? (int)(d + 2 * G * 64) : (int)(d + 128);
+        UP(D.attn_norm, L.attn_norm, d)
+        UP(D.post_attn_norm, L.post_attn_norm, d)
+        UP(D.ffn_norm, L.ffn_norm, d)
+        UP(D.post_ffn_norm, L.post_ffn_norm, d)
+        UP(D.qkv_w, L.qkv_w, (size_t)D.qkv_n * d)
+        UP(D.out_w, L.out_w, d * d)
+        // gate/up interleave in groups of 32 rows so one 64-wide GEMM tile holds matching pairs
+        for (size_t grp = 0; grp < F / 32; grp++) {
+            memcpy(&perm[(grp * 64) * d], L.up_w + (grp * 32) * d, 32 * d);
+            memcpy(&perm[(grp * 64 + 32) * d], L.up_w + (F + grp * 32) * d, 32 * d);
+        }
+        UP(D.up_w, perm.data(), 2 * F * d)
+        UP(D.down_w, L.down_w, d * F)
+        UP(D.score_mult, L.score_mult, (size_t)w->n_heads)
+        if (L.sink_key) { UP(D.sink, L.sink_key, 64) }
+        D.qkv_mult = L.qkv_mult; D.out_mult = L.out_mult; D.up_mult = L.up_mult; D.down_mult = L.down_mult;
+        D.qkv_shift = L.qkv_shift; D.out_shift = L.out_shift; D.up_shift = L.up_shift; D.down_shift = L.down_shift;
+    }
+#undef UP
+    *out = c.release();
+    return CZIP_OK;
+}
+
+extern "C" void czip_destroy(czip_ctx* c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    if (c->stream) hipStreamSynchronize(c->stream);
+    for (auto& p : c->pending) { hipEventDestroy(p.a); hipEventDestroy(p.b); }
+    for (auto e : c->event_pool) hipEventDestroy(e);
+    for (void* p : c->allocs) hipFree(p);
+    if (c->stream) hipStreamDestroy(c->stream);
+    delete c;
+}
+
+extern "C" void czip_set_profiling(czip_ctx* c, int32_t on) {
+    if (c) c->profiling = on != 0;
+}
+
+extern "C" czip_status czip_kernel_stats(czip_ctx* c, const char* name, int64_t* launches, double* total_ms) {
+    if (!c || !name) return CZIP_E_ARG;
+    auto it = c->stats.find(name);
+    if (launches) *launches = it == c->stats.end() ? 0 : it->second.launches;
+    if (total_ms) *total_ms = it == c->stats.end() ? 0.0 : it->second.ms;
+    return CZIP_OK;
+}
+
+extern "C" void czip_reset_stats(czip_ctx* c) {
+    if (c) c->stats.clear();
+}
+
+// ===========================================================================
+// Forward pass over a batch of chunks (shared by every entry point)
+// ===========================================================================
+namespace {
+
+size_t row_bytes(const czip_ctx* c) {
+    const size_t d = (size_t)c->cfg.d_model, F = (size_t)c->cfg.d_ff, V = (size_t)c->cfg.vocab;
+    return 4 * d /*x*/ + 5 * d /*xn q8 attn y8*/ + F /*r8*/ + 4 * V /*logits*/ + 8 /*lohi*/ + 8 /*inp tgt*/ +
+           2 * (size_t)c->KH * 64 /*kv*/ + 64;
+}
+
+czip_status alloc_scratch(czip_ctx* c, czip_job* j, int BC, int T) {
+    const size_t M = (size_t)BC * T;
+    const size_t d = (size_t)c->cfg.d_model, F = (size_t)c->cfg.d_ff, V = (size_t)c->cfg.vocab;
+    czip_status rc;
+    if ((rc = dalloc(c, j->allocs, &j->inp, M))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->tgt, M))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->lohi, 2 * M))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->lens, (size_t)BC))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->x, M * d))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->xn, M * d))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->q8, M * d))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->attn, M * d))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->y8, M * d))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->r8, M * F))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->kc, M * (size_t)c->KH * 64))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->vc, M * (size_t)c->KH * 64))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->logits, M * V))) return rc;
+    return CZIP_OK;
+}
+
+int pick_batch_chunks(const czip_ctx* c, int64_t nchunks, int T) {
+    double gb = 16.0;
+    if (const char* s = getenv("CZIP_SCRATCH_GB")) gb = atof(s);
+    double per_chunk = (double)row_bytes(c) * T;
+    int64_t bc = (int64_t)(gb * 1e9 / per_chunk);
+    bc = std::max<int64_t>(1, std::min<int64_t>(bc, nchunks));
+    return (int)bc;
+}
+
+// Run every layer on rows [0, nb*T) whose inputs are j->inp / j->lens; leaves
+// logits in j->logits.  (model.rs:362-480 as batched launches)
+czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T) {
+    const int M = nb * T;
+    const int d = c->cfg.d_model, F = c->cfg.d_ff, V = c->cfg.vocab, H = c->cfg.n_heads;
+    hipStream_t s = c->stream;
+    {
+        Timed t(c, "embed_norm");
+        launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, M, d, j->x, j->xn, s);
+    }
+    for (int l = 0; l < c->cfg.n_layers; l++) {
+        const DevLayer& L = c->layers[(size_t)l];
+        GemmArgs g{};
+        g.A = j->xn; g.W = L.qkv_w; g.M = M; g.N = L.qkv_n; g.K = d;
+        g.out8 = j->q8; g.ldo = d; g.mult = L.qkv_mult; g.shift = L.qkv_shift;
+        g.d = d; g.T = T; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads; g.KH = c->KH;
+        g.kc = j->kc; g.vc = j->vc; g.rcos = c->rcos; g.rsin = c->rsin;
+        { Timed t(c, "gemm_qkv"); launch_gemm(g, EPI_QKV, s); }
+        AttnArgs a{};
+        a.q = j->q8; a.kc = j->kc; a.vc = j->vc; a.lens = j->lens; a.score_mult = L.score_mult; a.sink = L.sink;
+        a.lut = c->lut; a.out = j->attn; a.M = M; a.T = T; a.H = H; a.G = c->cfg.n_kv_heads; a.KH = c->KH;
+        a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
+        { Timed t(c, "attention"); launch_attention(a, s); }
+        GemmArgs o{};
+        o.A = j->attn; o.W = L.out_w; o.M = M; o.N = d; o.K = d; o.out8 = j->y8; o.ldo = d;
+        o.mult = L.out_mult; o.shift = L.out_shift;
+        { Timed t(c, "gemm_o"); launch_gemm(o, EPI_REQ, s); }
+        { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.ffn_norm, L.post_attn_norm, M, d, j->xn, s); }
+        GemmArgs u{};
+        u.A = j->xn; u.W = L.up_w; u.M = M; u.N = 2 * F; u.K = d; u.out8 = j->r8; u.ldo = F;
+        u.mult = L.up_mult; u.shift = L.up_shift;
+        { Timed t(c, "gemm_up"); launch_gemm(u, EPI_REGLU, s); }
+        GemmArgs dn{};
+        dn.A = j->r8; dn.W = L.down_w; dn.M = M; dn.N = d; dn.K = F; dn.out8 = j->y8; dn.ldo = d;
+        dn.mult = L.down_mult; dn.shift = L.down_shift;
+        { Timed t(c, "gemm_down"); launch_gemm(dn, EPI_REQ, s); }
+        const int8_t* next = (l + 1 < c->cfg.n_layers) ? c->layers[(size_t)l + 1].attn_norm : c->final_norm;
+        { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.post_ffn_norm, next, M, d, j->xn, s); }
+    }
+    GemmArgs h{};
+    h.A = j->xn; h.W = c->head_w; h.M = M; h.N = V; h.K = d; h.out32 = j->logits; h.ldo = V;
+    { Timed t(c, "gemm_head"); launch_gemm(h, EPI_RAW, s); }
+    return CZIP_OK;
+}
+
+czip_status check_lens(czip_ctx* c, const int32_t* lens, int B, int T) {
+    if (T < 1) return fail(c, CZIP_E_ARG, "T must be >= 1");
+    if (T > c->cfg.context_length || T > c->cfg.max_seq_len)
+        return fail(c, CZIP_E_RANGE, "chunk length exceeds the RoPE LUT / KV cache (lut.rs:169-177)");
+    for (int b = 0; b < B; b++)
+        if (lens[b] < 0 || lens[b] > T) return fail(c, CZIP_E_ARG, "lens[b] out of [0, T]");
+    return CZIP_OK;
+}
+
+czip_status check_tokens(czip_ctx* c, const uint32_t* t, int64_t n) {
+    for (int64_t i = 0; i < n; i++)
+        if (t[i] >= (uint32_t)c->cfg.vocab) return fail(c, CZIP_E_TOKEN, "token id >= vocab at index " + std::to_string(i));
+    return CZIP_OK;
+}
+
+void free_job_mem(czip_job* j) {
+    for (void* p : j->allocs) hipFree(p);
+    j->allocs.clear();
+}
+
+// Debug paths (forward_logits / prefill_cdf / prefill_cumfreqs): one job
+// over caller-given input rows, processed in sub-batches.
+czip_status run_rows(czip_ctx* c, const uint32_t* rows_in, const uint32_t* rows_tgt, const int32_t* lens, int B, int T,
+                     int mode, void* host_out) {
+    czip_status rc = check_lens(c, lens, B, T);
+    if (rc) return rc;
+    if ((rc = check_tokens(c, rows_in, (int64_t)B * T))) return rc;
+    if (rows_tgt && (rc = check_tokens(c, rows_tgt, (int64_t)B * T))) return rc;
+    HIPCHECK(c, hipSetDevice(c->device));
+    czip_job j;
+    j.ctx = c;
+    const int BC = pick_batch_chunks(c, B, T);
+    if ((rc = alloc_scratch(c, &j, BC, T))) { free_job_mem(&j); return rc; }
+    const int V = c->cfg.vocab;
+    uint32_t* dcum = nullptr;
+    if (mode == 2 && (rc = dalloc(c, j.allocs, &dcum, (size_t)BC * T * V))) { free_job_mem(&j); return rc; }
+    for (int b0 = 0; b0 < B && rc == 0; b0 += BC) {
+        const int nb = std::min(BC, B - b0);
+        const size_t M = (size_t)nb * T;
+        hipError_t e = hipMemcpyAsync(j.inp, rows_in + (size_t)b0 * T, M * 4, hipMemcpyHostToDevice, c->stream);
+        if (e == hipSuccess && rows_tgt)
+            e = hipMemcpyAsync(j.tgt, rows_tgt + (size_t)b0 * T, M * 4, hipMemcpyHostToDevice, c->stream);
+        if (e == hipSuccess) e = hipMemcpyAsync(j.lens, lens + b0, (size_t)nb * 4, hipMemcpyHostToDevice, c->stream);
+        if (e != hipSuccess) { rc = fail(c, CZIP_E_HIP, hipGetErrorString(e)); break; }
+        if ((rc = forward_batch(c, &j, nb, T))) break;
+        if (mode == 0) {
+            e = hipMemcpyAsync((int32_t*)host_out + (size_t)b0 * T * V, j.logits, M * V * 4, hipMemcpyDeviceToHost, c->stream);
+        } else if (mode == 1) {
+            { Timed t(c, "cdf"); launch_cdf(j.logits, (int)M, V, j.tgt, j.lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 0, j.lohi, c->stream); }
+            e = hipMemcpyAsync((uint32_t*)host_out + (size_t)b0 * T * 2, j.lohi, M * 8, hipMemcpyDeviceToHost, c->stream);
+        } else {
+            { Timed t(c, "cdf"); launch_cdf(j.logits, (int)M, V, nullptr, j.lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 1, dcum, c->stream); }
+            e = hipMemcpyAsync((uint32_t*)host_out + (size_t)b0 * T * V, dcum, M * V * 4, hipMemcpyDeviceToHost, c->stream);
+        }
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) { rc = fail(c, CZIP_E_HIP, hipGetErrorString(e)); break; }
+    }
+    resolve_events(c);
+    free_job_mem(&j);
+    if (rc) return rc;
+    // rows past each chunk's length are not computed: report zeros
+    for (int b = 0; b < B; b++)
+        for (int p = lens[b]; p < T; p++) {
+            size_t r = (size_t)b * T + p;
+            if (mode == 0) memset((int32_t*)host_out + r * V, 0, (size_t)V * 4);
+            else if (mode == 1) memset((uint32_t*)host_out + r * 2, 0, 8);
+            else memset((uint32_t*)host_out + r * V, 0, (size_t)V * 4);
+        }
+    return CZIP_OK;
+}
+
+}  // namespace
+
+extern "C" czip_status czip_forward_logits(czip_ctx* c, const uint32_t* inputs, const int32_t* lens, int32_t B,
+                                           int32_t T, int32_t* logits) {
+    if (!c || !inputs || !lens || !logits || B < 0) return c ? fail(c, CZIP_E_ARG, "null argument") : CZIP_E_ARG;
+    if (B == 0) return CZIP_OK;
+    return run_rows(c, inputs, nullptr, lens, B, T, 0, logits);
+}
+
+static czip_status inputs_from_targets(czip_ctx* c, const uint32_t* targets, const int32_t* lens, int B, int T,
+                                       std::vector<uint32_t>& inp) {
+    inp.assign((size_t)B * T, 0u);
+    for (int b = 0; b < B; b++)
+        for (int p = 0; p < lens[b] && p < T; p++) inp[(size_t)b * T + p] = p == 0 ? BOS : targets[(size_t)b * T + p - 1];
+    (void)c;
+    return CZIP_OK;
+}
+
+extern "C" czip_status czip_prefill_cdf(czip_ctx* c, const uint32_t* targets, const int32_t* lens, int32_t B,
+                                        int32_t T, uint32_t* cum_lohi) {
+    if (!c || !targets || !lens || !cum_lohi || B < 0) return c ? fail(c, CZIP_E_ARG, "null argument") : CZIP_E_ARG;
+    if (B == 0) return CZIP_OK;
+    czip_status rc = check_lens(c, lens, B, T);
+    if (rc) return rc;
+    std::vector<uint32_t> inp, tgt((size_t)B * T, 0u);
+    for (int b = 0; b < B; b++)
+        for (int p = 0; p < lens[b]; p++) tgt[(size_t)b * T + p] = targets[(size_t)b * T + p];
+    inputs_from_targets(c, tgt.data(), lens, B, T, inp);
+    return run_rows(c, inp.data(), tgt.data(), lens, B, T, 1, cum_lohi);
+}
+
+extern "C" czip_status czip_prefill_cumfreqs(czip_ctx* c, const uint32_t* inputs, const int32_t* lens, int32_t B,
+                                             int32_t T, uint32_t* cumfreqs) {
+    if (!c || !inputs || !lens || !cumfreqs || B < 0) return c ? fail(c, CZIP_E_ARG, "null argument") : CZIP_E_ARG;
+    if (B == 0) return CZIP_OK;
+    return run_rows(c, inputs, nullptr, lens, B, T, 2, cumfreqs);
+}
+
+// ===========================================================================
+// Compress job
+// ===========================================================================
+extern "C" int64_t czip_chunk_slot_bytes(int32_t chunk) {
+    // at most 32 coded bits per token (a frequency >= 1 of a total < 2^30,
+    // plus the renormalisation bit), the terminating bit and a partial byte
+    return (int64_t)chunk * 4 + 16;
+}
+
+extern "C" czip_status czip_compress_plan(czip_ctx* c, const uint32_t* tokens, int64_t n, int32_t chunk, czip_job** out) {
+    if (!c || !out || (n > 0 && !tokens) || n < 0) return c ? fail(c, CZIP_E_ARG, "bad argument") : CZIP_E_ARG;
+    *out = nullptr;
+    if (chunk < 1) return fail(c, CZIP_E_ARG, "chunk must be >= 1");
+    if (chunk > c->cfg.context_length || chunk > c->cfg.max_seq_len)
+        return fail(c, CZIP_E_RANGE, "chunk length exceeds the RoPE LUT / KV cache (lut.rs:169-177)");
+    czip_status rc = check_tokens(c, tokens, n);
+    if (rc) return rc;
+    HIPCHECK(c, hipSetDevice(c->device));
+    auto j = std::make_unique<czip_job>();
+    j->ctx = c;
+    j->kind = 0;
+    j->n_tokens = n;
+    j->T = chunk;
+    j->nchunks = (n + chunk - 1) / chunk;
+    j->slot = czip_chunk_slot_bytes(chunk);
+    const int64_t nch = std::max<int64_t>(j->nchunks, 1);
+    j->BC = pick_batch_chunks(c, nch, chunk);
+    if ((rc = dalloc(c, j->allocs, &j->tok, (size_t)std::max<int64_t>(n, 1)))) { free_job_mem(j.get()); return rc; }
+    if ((rc = dalloc(c, j->allocs, &j->out, (size_t)(nch * j->slot)))) { free_job_mem(j.get()); return rc; }
+    if ((rc = dalloc(c, j->allocs, &j->out_lens, (size_t)nch))) { free_job_mem(j.get()); return rc; }
+    if ((rc = dalloc(c, j->allocs, &j->err, 1))) { free_job_mem(j.get()); return rc; }
+    if ((rc = alloc_scratch(c, j.get(), j->BC, chunk))) { free_job_mem(j.get()); return rc; }
+    if (n > 0) {
+        hipError_t e = hipMemcpy(j->tok, tokens, (size_t)n * 4, hipMemcpyHostToDevice);
+        if (e != hipSuccess) { free_job_mem(j.get()); return fail(c, CZIP_E_HIP, hipGetErrorString(e)); }
+    }
+    *out = j.release();
+    return CZIP_OK;
+}
+
+extern "C" int64_t czip_job_chunks(const czip_job* j) { return j ? j->nchunks : 0; }
+
+static czip_status run_compress(czip_job* j) {
+    czip_ctx* c = j->ctx;
+    hipStream_t s = c->stream;
+    const int T = j->T, V = c->cfg.vocab;
+    HIPCHECK(c, hipMemsetAsync(j->err, 0, 4, s));
+    for (int64_t c0 = 0; c0 < j->nchunks; c0 += j->BC) {
+        const int nb = (int)std::min<int64_t>(j->BC, j->nchunks - c0);
+        const int M = nb * T;
+        { Timed t(c, "prep"); launch_prep_chunks(j->tok, j->n_tokens, c0, nb, T, j->inp, j->tgt, j->lens, s); }
+        czip_status rc = forward_batch(c, j, nb, T);
+        if (rc) return rc;
+        { Timed t(c, "cdf"); launch_cdf(j->logits, M, V, j->tgt, j->lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 0, j->lohi, s); }
+        { Timed t(c, "encode"); launch_encode(j->lohi, j->lens, nb, T, c->cfg.target_total, j->out + c0 * j->slot, j->slot, j->out_lens + c0, j->err, s); }
+    }
+    HIPCHECK(c, hipGetLastError());
+    HIPCHECK(c, hipStreamSynchronize(s));
+    resolve_events(c);
+    int32_t err = 0;
+    HIPCHECK(c, hipMemcpy(&err, j->err, 4, hipMemcpyDeviceToHost));
+    if (err) return fail(c, CZIP_E_OVERFLOW, "coded chunk exceeded its slot");
+    return CZIP_OK;
+}
+
+extern "C" czip_status czip_job_run(czip_job* j) {
+    if (!j) return CZIP_E_ARG;
+    HIPCHECK(j->ctx, hipSetDevice(j->ctx->device));
+    if (j->kind == 0) return run_compress(j);
+    return fail(j->ctx, CZIP_E_ARG, "unknown job kind");
+}
+
+extern "C" czip_status czip_compress_fetch(czip_job* j, uint8_t* out, int64_t slot, int32_t* lens) {
+    if (!j || j->kind != 0 || !lens || (j->nchunks > 0 && !out)) return CZIP_E_ARG;
+    czip_ctx* c = j->ctx;
+    if (j->nchunks == 0) return CZIP_OK;
+    HIPCHECK(c, hipMemcpy(lens, j->out_lens, (size_t)j->nchunks * 4, hipMemcpyDeviceToHost));
+    for (int64_t i = 0; i < j->nchunks; i++)
+        if (lens[i] > slot) return fail(c, CZIP_E_OVERFLOW, "caller slot smaller than a coded chunk");
+    if (slot == j->slot) {
+        HIPCHECK(c, hipMemcpy(out, j->out, (size_t)(j->nchunks * j->slot), hipMemcpyDeviceToHost));
+    } else {
+        HIPCHECK(c, hipMemcpy2D(out, (size_t)slot, j->out, (size_t)j->slot, (size_t)std::min(slot, j->slot),
+                                (size_t)j->nchunks, hipMemcpyDeviceToHost));
+    }
+    return CZIP_OK;
+}
+
+extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t*, const int64_t*, const int32_t*, const int32_t*,
+                                            int32_t, czip_job** out) {
+    if (out) *out = nullptr;
+    return c ? fail(c, CZIP_E_ARG, "decompress is not built yet") : CZIP_E_ARG;
+}
+
+extern "C" czip_status czip_decompress_fetch(czip_job*, uint32_t*, const int64_t*) { return CZIP_E_ARG; }
+
+extern "C" void czip_job_free(czip_job* j) {
+    if (!j) return;
+    hipSetDevice(j->ctx->device);
+    hipStreamSynchronize(j->ctx->stream);
+    free_job_mem(j);
+    delete j;
+}

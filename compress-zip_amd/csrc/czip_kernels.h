@@ -1,0 +1,60 @@
+// Kernel launchers of libczip_hip (device code lives in czip_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace czip {
+
+enum GemmEpi : int {
+    EPI_RAW = 0,    // int32 accumulators (LM head logits, model.rs:477)
+    EPI_REQ = 1,    // requantize to int8 (model.rs:280-300)
+    EPI_QKV = 2,    // requantize + RoPE(Q, two roundings) / RoPE(K) + KV scatter
+    EPI_REGLU = 3,  // requantize gate/up pairs + ReGLU (reglu.rs:20-46)
+};
+
+struct GemmArgs {
+    const int8_t* A;  // [M, K] row-major
+    const int8_t* W;  // [N, K] row-major (PyTorch "TN")
+    int M, N, K;
+    int32_t* out32;   // EPI_RAW  [M, ldo]
+    int8_t* out8;     // EPI_REQ / EPI_REGLU / Q of EPI_QKV  [M, ldo]
+    int ldo;
+    int mult, shift;
+    // EPI_QKV
+    int d, T, kv_mode, G, KH;
+    int8_t* kc;       // [B, KH, T, 64]
+    int8_t* vc;
+    const int16_t* rcos;
+    const int16_t* rsin;
+};
+
+struct AttnArgs {
+    const int8_t* q;          // [M, H*64]  rotated + NET_SHIFT-ed queries
+    const int8_t* kc;         // [B, KH, T, 64]
+    const int8_t* vc;
+    const int32_t* lens;      // [B]
+    const int32_t* score_mult;// [H]
+    const int8_t* sink;       // [64] or nullptr
+    const uint16_t* lut;      // [256]
+    int8_t* out;              // [M, H*64]
+    int M, T, H, G, KH, kv_mode;
+    unsigned coef;
+};
+
+void launch_prep_chunks(const uint32_t* toks, int64_t n_tokens, int64_t chunk0, int nb, int T,
+                        uint32_t* inp, uint32_t* tgt, int32_t* lens, hipStream_t s);
+void launch_embed_norm(const uint32_t* inp, const int8_t* embed, const int8_t* w, int M, int d,
+                       int32_t* x, int8_t* xn, hipStream_t s);
+void launch_resid_norm(int32_t* x, const int8_t* y8, const int8_t* w1, const int8_t* w2, int M, int d,
+                       int8_t* xn, hipStream_t s);
+void launch_gemm(const GemmArgs& a, int epi, hipStream_t s);
+void launch_attention(const AttnArgs& a, hipStream_t s);
+// mode 0: (lo, hi) of targets; mode 1: full inclusive cumfreqs
+void launch_cdf(const int32_t* logits, int M, int V, const uint32_t* targets, const int32_t* lens, int T,
+                const uint16_t* lut, unsigned coef, unsigned total, int mode, uint32_t* out, hipStream_t s);
+void launch_encode(const uint32_t* lohi, const int32_t* lens, int nb, int T, unsigned total, uint8_t* out,
+                   int64_t slot, int32_t* out_lens, int32_t* err, hipStream_t s);
+
+}  // namespace czip

@@ -1,0 +1,256 @@
+"""Python mirror of the compress-zip model API over libczip_hip (MI355X).
+
+The reference exposes `ModelWeights::load` (rust/src/model.rs:108),
+`Model::new` (model.rs:315), `Model::forward` (model.rs:362) and
+`Model::get_cumfreqs` (model.rs:483), called once per token by the chunk
+loops of rust/src/main.rs:206-238 / 377-396.  This module binds the batched
+C-ABI of include/czip_hip.h that replaces those calls: whole chunks run as
+one causal prefill on the GPU, and compression (forward -> CDF -> arithmetic
+coding) runs end to end on the device.
+
+There is no CPU fallback: every compute call goes to the HIP library, and
+importing this module fails if the library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from .build import LIB_PATH
+
+KV_RUST_COMPAT = 0
+KV_GQA = 1
+BOS = 1022  # rust/src/main.rs:222
+
+STATUS = {
+    0: "OK", -1: "CZIP_E_ARG", -2: "CZIP_E_CONFIG", -3: "CZIP_E_HEADS", -4: "CZIP_E_RANGE", -5: "CZIP_E_TOKEN",
+    -6: "CZIP_E_OVERFLOW", -7: "CZIP_E_HIP", -8: "CZIP_E_IO", -9: "CZIP_E_MISSING", -10: "CZIP_E_NOMEM",
+    -11: "CZIP_E_FORMAT",
+}
+
+
+class CzipError(RuntimeError):
+    def __init__(self, code: int, msg: str = ""):
+        self.code = code
+        super().__init__(f"{STATUS.get(code, code)}: {msg}")
+
+
+class LayerDesc(C.Structure):
+    _fields_ = [
+        ("attn_norm", C.c_void_p), ("post_attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p),
+        ("post_ffn_norm", C.c_void_p), ("qkv_w", C.c_void_p), ("out_w", C.c_void_p), ("up_w", C.c_void_p),
+        ("down_w", C.c_void_p), ("score_mult", C.c_void_p), ("sink_key", C.c_void_p),
+        ("qkv_mult", C.c_int32), ("out_mult", C.c_int32), ("up_mult", C.c_int32), ("down_mult", C.c_int32),
+        ("qkv_shift", C.c_int32), ("out_shift", C.c_int32), ("up_shift", C.c_int32), ("down_shift", C.c_int32),
+    ]
+
+
+class ModelDesc(C.Structure):
+    _fields_ = [
+        ("vocab", C.c_int32), ("n_layers", C.c_int32), ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32),
+        ("d_model", C.c_int32), ("d_ff", C.c_int32), ("head_dim", C.c_int32), ("max_seq_len", C.c_int32),
+        ("context_length", C.c_int32), ("kv_mode", C.c_int32),
+        ("embed", C.c_void_p), ("final_norm", C.c_void_p), ("head_w", C.c_void_p), ("exp2_lut", C.c_void_p),
+        ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
+        ("coef_q24", C.c_uint32), ("target_total", C.c_uint32),
+        ("layers", C.POINTER(LayerDesc)),
+        ("exp2_len", C.c_int64), ("rope_len", C.c_int64),
+    ]
+
+
+# Functions declared in include/czip_hip.h, with their ctypes signatures.
+_P = C.c_void_p
+SIGNATURES = {
+    "czip_model_load": (C.c_int32, [C.c_char_p, C.c_int32, C.POINTER(C.c_void_p)]),
+    "czip_model_desc_get": (C.POINTER(ModelDesc), [_P]),
+    "czip_model_tokenizer": (C.c_void_p, [_P, C.POINTER(C.c_size_t), C.POINTER(C.c_char_p)]),
+    "czip_model_free": (None, [_P]),
+    "czip_create": (C.c_int32, [C.POINTER(ModelDesc), C.c_int, C.POINTER(C.c_void_p)]),
+    "czip_destroy": (None, [_P]),
+    "czip_last_error": (C.c_char_p, [_P]),
+    "czip_device_count": (C.c_int, []),
+    "czip_forward_logits": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
+    "czip_prefill_cdf": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
+    "czip_prefill_cumfreqs": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
+    "czip_compress_plan": (C.c_int32, [_P, _P, C.c_int64, C.c_int32, C.POINTER(C.c_void_p)]),
+    "czip_job_run": (C.c_int32, [_P]),
+    "czip_job_chunks": (C.c_int64, [_P]),
+    "czip_compress_fetch": (C.c_int32, [_P, _P, C.c_int64, _P]),
+    "czip_job_free": (None, [_P]),
+    "czip_chunk_slot_bytes": (C.c_int64, [C.c_int32]),
+    "czip_decompress_plan": (C.c_int32, [_P, _P, _P, _P, _P, C.c_int32, C.POINTER(C.c_void_p)]),
+    "czip_decompress_fetch": (C.c_int32, [_P, _P, _P]),
+    "czip_set_profiling": (None, [_P, C.c_int32]),
+    "czip_kernel_stats": (C.c_int32, [_P, C.c_char_p, C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
+    "czip_reset_stats": (None, [_P]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded libczip_hip.so.  Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libczip_hip.so not built ({LIB_PATH}); run __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def device_count() -> int:
+    return int(lib().czip_device_count())
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+class ModelWeights:
+    """A loaded .czm file (ModelWeights::load, rust/src/model.rs:108-274)."""
+
+    def __init__(self, path: str, kv_mode: int = KV_RUST_COMPAT):
+        self._h = C.c_void_p()
+        rc = lib().czip_model_load(os.fsencode(path), kv_mode, C.byref(self._h))
+        if rc:
+            raise CzipError(rc, f"loading {path}")
+        self.path = path
+        self.desc = lib().czip_model_desc_get(self._h).contents
+
+    @property
+    def config(self) -> dict:
+        d = self.desc
+        return dict(vocab_size=d.vocab, n_layers=d.n_layers, n_heads=d.n_heads, n_kv_heads=d.n_kv_heads,
+                    d_model=d.d_model, d_ff=d.d_ff, head_dim=d.head_dim, max_seq_len=d.max_seq_len,
+                    context_length=d.context_length, kv_mode=d.kv_mode, coef_q24=d.coef_q24,
+                    target_total=d.target_total)
+
+    def tokenizer_data(self):
+        n = C.c_size_t()
+        codec = C.c_char_p()
+        ptr = lib().czip_model_tokenizer(self._h, C.byref(n), C.byref(codec))
+        if not ptr:
+            return None, None
+        return C.string_at(ptr, n.value), codec.value.decode()
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().czip_model_free(self._h)
+            self._h = None
+
+
+class Model:
+    """Device context (Model::new, rust/src/model.rs:315-351) with batched
+    forward / CDF / compression entry points."""
+
+    def __init__(self, weights: ModelWeights, device: int = 0):
+        self._ctx = C.c_void_p()
+        self.weights = weights
+        rc = lib().czip_create(C.byref(weights.desc), device, C.byref(self._ctx))
+        if rc:
+            raise CzipError(rc, "czip_create")
+        self.vocab = weights.desc.vocab
+        self.target_total = weights.desc.target_total
+
+    def _check(self, rc: int):
+        if rc:
+            raise CzipError(rc, lib().czip_last_error(self._ctx).decode())
+
+    def close(self):
+        if getattr(self, "_ctx", None):
+            lib().czip_destroy(self._ctx)
+            self._ctx = None
+
+    def __del__(self):
+        self.close()
+
+    # --- batched forward (debug / parity) ---
+    def forward_logits(self, inputs: np.ndarray, lens) -> np.ndarray:
+        """inputs [B, T] token ids fed at positions 0..T-1 of each chunk -> logits [B, T, V]."""
+        inputs = np.ascontiguousarray(inputs, dtype=np.uint32)
+        B, T = inputs.shape
+        lens = np.ascontiguousarray(lens, dtype=np.int32)
+        out = np.zeros((B, T, self.vocab), np.int32)
+        self._check(lib().czip_forward_logits(self._ctx, _p(inputs), _p(lens), B, T, _p(out)))
+        return out
+
+    def cumfreqs(self, inputs: np.ndarray, lens) -> np.ndarray:
+        inputs = np.ascontiguousarray(inputs, dtype=np.uint32)
+        B, T = inputs.shape
+        lens = np.ascontiguousarray(lens, dtype=np.int32)
+        out = np.zeros((B, T, self.vocab), np.uint32)
+        self._check(lib().czip_prefill_cumfreqs(self._ctx, _p(inputs), _p(lens), B, T, _p(out)))
+        return out
+
+    def prefill_cdf(self, targets: np.ndarray, lens) -> np.ndarray:
+        """(cum_lo, cum_hi) [B, T, 2] of each target under its chunk's CDF."""
+        targets = np.ascontiguousarray(targets, dtype=np.uint32)
+        B, T = targets.shape
+        lens = np.ascontiguousarray(lens, dtype=np.int32)
+        out = np.zeros((B, T, 2), np.uint32)
+        self._check(lib().czip_prefill_cdf(self._ctx, _p(targets), _p(lens), B, T, _p(out)))
+        return out
+
+    # --- compression on the device ---
+    def compress_plan(self, tokens: np.ndarray, chunk: int) -> "Job":
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+        h = C.c_void_p()
+        self._check(lib().czip_compress_plan(self._ctx, _p(tokens) if tokens.size else None, tokens.size, chunk,
+                                             C.byref(h)))
+        return Job(self, h, chunk)
+
+    def compress_chunks(self, tokens: np.ndarray, chunk: int):
+        """Per-chunk coded bytes, identical to main.rs:206-238's chunk_results."""
+        job = self.compress_plan(tokens, chunk)
+        try:
+            job.run()
+            return job.fetch()
+        finally:
+            job.free()
+
+    # --- instrumentation ---
+    def set_profiling(self, on: bool):
+        lib().czip_set_profiling(self._ctx, 1 if on else 0)
+
+    def kernel_stats(self, name: str):
+        n = C.c_int64()
+        ms = C.c_double()
+        self._check(lib().czip_kernel_stats(self._ctx, name.encode(), C.byref(n), C.byref(ms)))
+        return int(n.value), float(ms.value)
+
+    def reset_stats(self):
+        lib().czip_reset_stats(self._ctx)
+
+
+class Job:
+    def __init__(self, model: Model, handle, chunk: int):
+        self.model = model
+        self.h = handle
+        self.chunk = chunk
+        self.nchunks = int(lib().czip_job_chunks(handle))
+
+    def run(self):
+        self.model._check(lib().czip_job_run(self.h))
+
+    def fetch(self):
+        slot = int(lib().czip_chunk_slot_bytes(self.chunk))
+        buf = np.zeros(max(self.nchunks, 1) * slot, np.uint8)
+        lens = np.zeros(max(self.nchunks, 1), np.int32)
+        self.model._check(lib().czip_compress_fetch(self.h, _p(buf), slot, _p(lens)))
+        return [bytes(buf[c * slot:c * slot + lens[c]]) for c in range(self.nchunks)]
+
+    def free(self):
+        if self.h:
+            lib().czip_job_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.free()

@@ -1,0 +1,153 @@
+/*
+ * czip_hip.h -- C-ABI of the MI355X (gfx950) integer-transformer path of
+ * compress-zip: batched causal prefill -> quantized CDF -> arithmetic coding
+ * (compress), and batched multi-stream decode (decompress).
+ *
+ * Plain C types only; no exceptions or aborts cross this boundary.  Every
+ * entry point returns czip_status (0 = OK, negative = error class) and leaves
+ * a message retrievable with czip_last_error().  A context owns one HIP
+ * stream and all device memory it allocates; it is not thread-safe, but
+ * several contexts may coexist (one per host thread / device).
+ *
+ * The reference has no FFI; each entry point names the Rust API it stands in
+ * for (file:line in the reference crate, rust/src).
+ */
+#ifndef CZIP_HIP_H
+#define CZIP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t czip_status;
+#define CZIP_OK            0
+#define CZIP_E_ARG        -1  /* bad argument / null pointer / bad sizes        */
+#define CZIP_E_CONFIG     -2  /* unsupported model shape (head_dim != 64, ...)  */
+#define CZIP_E_HEADS      -3  /* n_heads not in {4,6,8} in rust-compat KV mode  */
+                              /*   (the panic of rust/src/attention.rs:172)     */
+#define CZIP_E_RANGE      -4  /* position past the RoPE LUT / KV cache          */
+                              /*   (the index panics of lut.rs:169-177)         */
+#define CZIP_E_TOKEN      -5  /* token id >= vocab                              */
+#define CZIP_E_OVERFLOW   -6  /* coded chunk larger than its output slot        */
+#define CZIP_E_HIP        -7  /* HIP runtime failure                            */
+#define CZIP_E_IO         -8  /* file open/read/parse failure                   */
+#define CZIP_E_MISSING    -9  /* required tensor absent (model.rs:152-154)      */
+#define CZIP_E_NOMEM     -10  /* device or host allocation failed               */
+#define CZIP_E_FORMAT    -11  /* malformed container / LUT size mismatch        */
+
+/* KV-cache semantics.  RUST_COMPAT reproduces gqa_attention_mqa_i8
+ * (rust/src/attention.rs:162-289): one cached head, K = the first kv head's
+ * K slice and V = the next 64 values of the QKV row.  GQA is the extension
+ * where query head h reads kv head floor(h*G/H) with its own K and V. */
+#define CZIP_KV_RUST_COMPAT 0
+#define CZIP_KV_GQA         1
+
+/* Host pointers to one layer's tensors (rust/src/model.rs:52-83). */
+typedef struct czip_layer_desc {
+    const int8_t*  attn_norm;       /* [d]          */
+    const int8_t*  post_attn_norm;  /* [d]          */
+    const int8_t*  ffn_norm;        /* [d]          */
+    const int8_t*  post_ffn_norm;   /* [d]          */
+    const int8_t*  qkv_w;           /* [d+2*G*64,d] */
+    const int8_t*  out_w;           /* [d,d]        */
+    const int8_t*  up_w;            /* [2F,d] gate rows then up rows */
+    const int8_t*  down_w;          /* [d,F]        */
+    const int32_t* score_mult;      /* [H]          */
+    const int8_t*  sink_key;        /* [64] or NULL */
+    int32_t qkv_mult, out_mult, up_mult, down_mult;
+    int32_t qkv_shift, out_shift, up_shift, down_shift;
+} czip_layer_desc;
+
+/* Host pointers + config of a whole model (rust/src/model.rs:19-48, 86-104). */
+typedef struct czip_model_desc {
+    int32_t vocab, n_layers, n_heads, n_kv_heads, d_model, d_ff, head_dim;
+    int32_t max_seq_len, context_length, kv_mode;
+    const int8_t*   embed;          /* [V,d]  */
+    const int8_t*   final_norm;     /* [d]    */
+    const int8_t*   head_w;         /* [V,d]  */
+    const uint16_t* exp2_lut;       /* [256]  */
+    const int16_t*  rope_cos;       /* [context_length,32] */
+    const int16_t*  rope_sin;       /* [context_length,32] */
+    uint32_t coef_q24, target_total;
+    const czip_layer_desc* layers;  /* [n_layers] */
+    int64_t exp2_len;               /* entries of exp2_lut (must be 256)            */
+    int64_t rope_len;               /* entries of each RoPE table (context_length*32) */
+} czip_model_desc;
+
+typedef struct czip_model czip_model;   /* host-side loaded .czm file     */
+typedef struct czip_ctx   czip_ctx;     /* device-side weights + stream   */
+typedef struct czip_job   czip_job;     /* device buffers of one workload */
+
+/* ---- host loader: replaces ModelWeights::load (rust/src/model.rs:108-274,
+ *      rust/src/safetensors.rs:287-376).  Metadata defaults follow
+ *      model.rs:113-145, scalar defaults model.rs:157-168. ---- */
+czip_status czip_model_load(const char* path, int32_t kv_mode, czip_model** out);
+const czip_model_desc* czip_model_desc_get(const czip_model* m);
+/* Embedded tokenizer bytes (tensor "tokenizer.data"), NULL if absent. */
+const uint8_t* czip_model_tokenizer(const czip_model* m, size_t* len, const char** codec);
+void czip_model_free(czip_model* m);
+
+/* ---- device context: replaces Model::new (rust/src/model.rs:315-351).
+ *      Validates LUT sizes (model.rs:324-333) and head constraints
+ *      (attention.rs:172).  Weights are copied; the caller keeps ownership. ---- */
+czip_status czip_create(const czip_model_desc* w, int device, czip_ctx** out);
+void        czip_destroy(czip_ctx* ctx);
+const char* czip_last_error(const czip_ctx* ctx);   /* never NULL */
+int         czip_device_count(void);
+
+/* ---- debug / parity: logits of B chunks of T tokens (Model::forward,
+ *      rust/src/model.rs:362-480, called at positions 0..lens[b]-1 with
+ *      inputs[b*T + p]).  logits: host [B*T, V]; rows p >= lens[b] are 0. ---- */
+czip_status czip_forward_logits(czip_ctx* ctx, const uint32_t* inputs, const int32_t* lens,
+                                int32_t B, int32_t T, int32_t* logits);
+
+/* ---- compress, per-token CDF only: for each chunk b and position p <
+ *      lens[b], the coder interval of targets[b*T+p] under the CDF that
+ *      Model::get_cumfreqs (model.rs:483-486, softmax_cdf.rs:85-139) builds
+ *      from forward(prev, p) with prev = 1022 at p = 0 (main.rs:220-226).
+ *      cum_lohi: host [B*T, 2] = (cum[tok-1] or 0, cum[tok]); the total is
+ *      the model's target_total.  This is what a Rust caller binds when it
+ *      keeps its own ArithEncoder (arith_coder.rs:80-98). ---- */
+czip_status czip_prefill_cdf(czip_ctx* ctx, const uint32_t* targets, const int32_t* lens,
+                             int32_t B, int32_t T, uint32_t* cum_lohi);
+
+/* Full cumulative tables (debug / parity), host [B*T, V]. */
+czip_status czip_prefill_cumfreqs(czip_ctx* ctx, const uint32_t* inputs, const int32_t* lens,
+                                  int32_t B, int32_t T, uint32_t* cumfreqs);
+
+/* ---- compress end to end on the device: the rayon chunk loop of
+ *      main.rs:206-238 (fresh model per chunk, BOS=1022, pos restarts at 0,
+ *      encoder.finish per chunk) with forward, CDF and arithmetic coding all
+ *      on the GPU.  Chunk c covers tokens[c*chunk .. min((c+1)*chunk, n)). ---- */
+czip_status czip_compress_plan(czip_ctx* ctx, const uint32_t* tokens, int64_t n_tokens,
+                               int32_t chunk, czip_job** job);
+czip_status czip_job_run(czip_job* job);          /* device work only, synchronous */
+int64_t     czip_job_chunks(const czip_job* job);
+/* Coded bytes of every chunk into out[c*slot ..], lengths into lens[c]. */
+czip_status czip_compress_fetch(czip_job* job, uint8_t* out, int64_t slot, int32_t* lens);
+void        czip_job_free(czip_job* job);
+/* Upper bound of one chunk's coded size for `chunk` tokens. */
+int64_t     czip_chunk_slot_bytes(int32_t chunk);
+
+/* ---- decompress end to end on the device: the chunk loop of
+ *      main.rs:377-396 (ArithDecoder per chunk, arith_coder.rs:153-264) run
+ *      as batched autoregressive decode, one token per stream per step. ---- */
+czip_status czip_decompress_plan(czip_ctx* ctx, const uint8_t* data, const int64_t* offs,
+                                 const int32_t* lens, const int32_t* ntoks, int32_t nchunks,
+                                 czip_job** job);
+czip_status czip_decompress_fetch(czip_job* job, uint32_t* tokens_out, const int64_t* tok_offs);
+
+/* ---- instrumentation: per-kernel HIP-event timing on the context stream. ---- */
+void        czip_set_profiling(czip_ctx* ctx, int32_t on);
+/* Kernel names: "embed_norm","gemm_qkv","attention","gemm_o","row_norm",
+ * "gemm_up","gemm_down","gemm_head","cdf","encode", decode kernels ... */
+czip_status czip_kernel_stats(czip_ctx* ctx, const char* name, int64_t* launches, double* total_ms);
+void        czip_reset_stats(czip_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
