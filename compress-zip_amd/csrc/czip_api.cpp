@@ -512,6 +512,7 @@ extern "C" czip_status czip_compress_plan(czip_ctx* c, const uint32_t* tokens, i
     if (chunk < 1) return fail(c, CZIP_E_ARG, "chunk must be >= 1");
     if (chunk > c->cfg.context_length || chunk > c->cfg.max_seq_len)
         return fail(c, CZIP_E_RANGE, "chunk length exceeds the RoPE LUT / KV cache (lut.rs:169-177)");
+    if ((uint32_t)c->cfg.vocab <= BOS) return fail(c, CZIP_E_TOKEN, "BOS token 1022 is outside the vocabulary");
     czip_status rc = check_tokens(c, tokens, n);
     if (rc) return rc;
     HIPCHECK(c, hipSetDevice(c->device));

@@ -502,7 +502,7 @@ __global__ __launch_bounds__(CDF_THREADS) void k_cdf(const int32_t* __restrict__
             out[(size_t)row * 2 + 1] = lo + f;
         }
     } else {
-        unsigned run = excl;
+        unsigned run = excl + (am < i0 ? rem : 0u);
         for (int k = 0; k < per; k++) {
             int i = i0 + k;
             if (i >= V) break;

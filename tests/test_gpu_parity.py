@@ -107,7 +107,7 @@ def random_models(tmp_path_factory):
         "d768": synth.write_random_model(str(d / "d768.czm"), d=768, n_layers=2, n_heads=12, n_kv=4, d_ff=3072,
                                          vocab=8192, ctx=4096, seed=22),
         "sink": synth.write_random_model(str(d / "sink.czm"), d=256, n_layers=2, n_heads=4, n_kv=1, d_ff=512,
-                                         vocab=512, ctx=256, seed=23, sink=True),
+                                         vocab=1024, ctx=256, seed=23, sink=True),
     }
     return paths
 
@@ -129,7 +129,7 @@ def test_random_d768_gqa(amd, orc, random_models):
 
 def test_random_sink_compat(amd, orc, random_models):
     gm, om = _model_pair(amd, orc, random_models["sink"], amd.KV_RUST_COMPAT)
-    _check_logits(gm, om, 128, [128, 5], 34, 512)
+    _check_logits(gm, om, 128, [128, 5], 34, 1024)
 
 
 def test_compress_random_d512(amd, orc, random_models):
