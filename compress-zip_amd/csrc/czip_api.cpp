@@ -308,6 +308,8 @@ extern "C" void czip_reset_stats(czip_ctx* c) {
 // ===========================================================================
 namespace {
 
+int pad64(int T) { return (T + 63) & ~63; }
+
 size_t row_bytes(const czip_ctx* c) {
     const size_t d = (size_t)c->cfg.d_model, F = (size_t)c->cfg.d_ff, V = (size_t)c->cfg.vocab;
     return 4 * d /*x*/ + 5 * d /*xn q8 attn y8*/ + F /*r8*/ + 4 * V /*logits*/ + 8 /*lohi*/ + 8 /*inp tgt*/ +
@@ -329,7 +331,7 @@ czip_status alloc_scratch(czip_ctx* c, czip_job* j, int BC, int T) {
     if ((rc = dalloc(c, j->allocs, &j->y8, M * d))) return rc;
     if ((rc = dalloc(c, j->allocs, &j->r8, M * F))) return rc;
     if ((rc = dalloc(c, j->allocs, &j->kc, M * (size_t)c->KH * 64))) return rc;
-    if ((rc = dalloc(c, j->allocs, &j->vc, M * (size_t)c->KH * 64))) return rc;
+    if ((rc = dalloc(c, j->allocs, &j->vc, (size_t)BC * pad64(T) * (size_t)c->KH * 64))) return rc;
     if ((rc = dalloc(c, j->allocs, &j->logits, M * V))) return rc;
     return CZIP_OK;
 }
@@ -358,14 +360,14 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T) {
         GemmArgs g{};
         g.A = j->xn; g.W = L.qkv_w; g.M = M; g.N = L.qkv_n; g.K = d;
         g.out8 = j->q8; g.ldo = d; g.mult = L.qkv_mult; g.shift = L.qkv_shift;
-        g.d = d; g.T = T; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads; g.KH = c->KH;
+        g.d = d; g.T = T; g.TP = pad64(T); g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads; g.KH = c->KH;
         g.kc = j->kc; g.vc = j->vc; g.rcos = c->rcos; g.rsin = c->rsin;
         { Timed t(c, "gemm_qkv"); launch_gemm(g, EPI_QKV, s); }
         AttnArgs a{};
-        a.q = j->q8; a.kc = j->kc; a.vc = j->vc; a.lens = j->lens; a.score_mult = L.score_mult; a.sink = L.sink;
-        a.lut = c->lut; a.out = j->attn; a.M = M; a.T = T; a.H = H; a.G = c->cfg.n_kv_heads; a.KH = c->KH;
-        a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
-        { Timed t(c, "attention"); launch_attention(a, s); }
+        a.q = j->q8; a.kc = j->kc; a.vc = j->vc; a.TP = pad64(T); a.lens = j->lens; a.score_mult = L.score_mult;
+        a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = M; a.T = T; a.H = H; a.G = c->cfg.n_kv_heads;
+        a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
+        { Timed t(c, "attention"); launch_attention(a, nb, s); }
         GemmArgs o{};
         o.A = j->attn; o.W = L.out_w; o.M = M; o.N = d; o.K = d; o.out8 = j->y8; o.ldo = d;
         o.mult = L.out_mult; o.shift = L.out_shift;

@@ -24,8 +24,9 @@ struct GemmArgs {
     int mult, shift;
     // EPI_QKV
     int d, T, kv_mode, G, KH;
-    int8_t* kc;       // [B, KH, T, 64]
-    int8_t* vc;
+    int TP;           // V^T row stride: T rounded up to a multiple of 64
+    int8_t* kc;       // [B, KH, T, 64]   rotated keys
+    int8_t* vc;       // [B, KH, 64, TP]  values, transposed (dim-major)
     const int16_t* rcos;
     const int16_t* rsin;
 };
@@ -33,7 +34,8 @@ struct GemmArgs {
 struct AttnArgs {
     const int8_t* q;          // [M, H*64]  rotated + NET_SHIFT-ed queries
     const int8_t* kc;         // [B, KH, T, 64]
-    const int8_t* vc;
+    const int8_t* vc;         // [B, KH, 64, TP]
+    int TP;
     const int32_t* lens;      // [B]
     const int32_t* score_mult;// [H]
     const int8_t* sink;       // [64] or nullptr
@@ -50,7 +52,7 @@ void launch_embed_norm(const uint32_t* inp, const int8_t* embed, const int8_t* w
 void launch_resid_norm(int32_t* x, const int8_t* y8, const int8_t* w1, const int8_t* w2, int M, int d,
                        int8_t* xn, hipStream_t s);
 void launch_gemm(const GemmArgs& a, int epi, hipStream_t s);
-void launch_attention(const AttnArgs& a, hipStream_t s);
+void launch_attention(const AttnArgs& a, int B, hipStream_t s);
 // mode 0: (lo, hi) of targets; mode 1: full inclusive cumfreqs
 void launch_cdf(const int32_t* logits, int M, int V, const uint32_t* targets, const int32_t* lens, int T,
                 const uint16_t* lut, unsigned coef, unsigned total, int mode, uint32_t* out, hipStream_t s);

@@ -252,7 +252,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    // N tiles vary fastest so consecutive workgroups reuse the same A rows from L2
+    const int ntn = (a.N + BN - 1) / BN;
+    const int m0 = (int)(blockIdx.x / ntn) * BM, n0 = (int)(blockIdx.x % ntn) * BN;
 
     v4i acc[4][4];
     for (int i = 0; i < 4; i++)
@@ -274,18 +276,23 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int col_base = n0 + wn * 64;  // 64-aligned, one head / one gate-up group
     if (col_base >= a.N) return;
     const int lc = lane & 15, lrow = (lane >> 4) * 4;
+#pragma unroll
     for (int i = 0; i < 4; i++) {
+#pragma unroll
         for (int r = 0; r < 4; r++) {
             const int row = m0 + wm * 64 + i * 16 + lrow + r;
             if (row >= a.M) continue;
             if (EPI == EPI_RAW) {
+#pragma unroll
                 for (int j = 0; j < 4; j++) a.out32[(size_t)row * a.ldo + col_base + j * 16 + lc] = acc[i][j][r];
             } else if (EPI == EPI_REQ) {
+#pragma unroll
                 for (int j = 0; j < 4; j++)
                     a.out8[(size_t)row * a.ldo + col_base + j * 16 + lc] = (int8_t)requant(acc[i][j][r], a.mult, a.shift);
             } else if (EPI == EPI_REGLU) {
                 // W rows were permuted so that a 64-row group holds 32 gate rows then the
                 // matching 32 up rows: output feature f = col_base/2 + j*16 + lc.
+#pragma unroll
                 for (int j = 0; j < 2; j++) {
                     int g = requant(acc[i][j][r], a.mult, a.shift);
                     int u = requant(acc[i][j + 2][r], a.mult, a.shift);
@@ -294,6 +301,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                 }
             } else {  // EPI_QKV
                 const int p = row % a.T, b = row / a.T;
+#pragma unroll
                 for (int j = 0; j < 2; j++) {
                     const int i32 = j * 16 + lc;  // rotary pair (i32, i32 + 32)
                     const int xv = requant(acc[i][j][r], a.mult, a.shift);
@@ -311,14 +319,16 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                         int g, isv;
                         if (a.kv_mode == 1) { isv = kcol >= 64 * a.G; g = (isv ? kcol - 64 * a.G : kcol) >> 6; }
                         else { isv = kcol >= 64; g = 0; }
-                        size_t off = (((size_t)b * a.KH + g) * a.T + p) * 64;
                         if (!isv) {
                             // K: attention.rs:29-50
+                            size_t off = (((size_t)b * a.KH + g) * a.T + p) * 64;
                             a.kc[off + i32] = (int8_t)clamp127(sra_rne32(xr, 15));
                             a.kc[off + i32 + 32] = (int8_t)clamp127(sra_rne32(yr, 15));
                         } else {
-                            a.vc[off + i32] = (int8_t)xv;
-                            a.vc[off + i32 + 32] = (int8_t)yv;
+                            // V, stored dim-major for the PV operand
+                            size_t off = (((size_t)b * a.KH + g) * 64) * a.TP + p;
+                            a.vc[off + (size_t)i32 * a.TP] = (int8_t)xv;
+                            a.vc[off + (size_t)(i32 + 32) * a.TP] = (int8_t)yv;
                         }
                     }
                 }
@@ -328,7 +338,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 }
 
 void launch_gemm(const GemmArgs& a, int epi, hipStream_t s) {
-    dim3 grid((unsigned)((a.M + BM - 1) / BM), (unsigned)((a.N + BN - 1) / BN));
+    dim3 grid((unsigned)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN)));
     switch (epi) {
         case EPI_RAW: hipLaunchKernelGGL(k_gemm<EPI_RAW>, grid, dim3(256), 0, s, a); break;
         case EPI_REQ: hipLaunchKernelGGL(k_gemm<EPI_REQ>, grid, dim3(256), 0, s, a); break;
@@ -338,78 +348,234 @@ void launch_gemm(const GemmArgs& a, int epi, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Attention (reference-order online softmax), one wavefront per (row, head).
-// Lanes compute 64 scores at a time; the softmax update then walks the keys
-// in order with lanes = head dims, exactly as attention.rs:205-276.
+// Prefill attention, exact, on MFMA.
+//
+// The reference walks the keys of a query row in order, rescaling the running
+// sum S and the value accumulator with a rounded factor each time the running
+// max strictly increases (attention.rs:205-276).  Between two such "records"
+// every key's weight uses the same max, so the segment's contribution is a
+// plain integer sum (S in u64, vacc modulo 2^32) that can be formed in any
+// order.  Per 64-key tile the kernel therefore:
+//   1. forms S^T = K Q^T with int8 MFMA and applies the score epilogue;
+//   2. scans each row's keys in order for running max, records, weights
+//      w = E(s - max) and segment ids (lanes own 16 consecutive keys);
+//   3. for each segment j = 0..max records, accumulates O^T += V^T P_j^T on
+//      int8 MFMA (P_j = weights of segment j, split into three 7-bit limbs),
+//      rescaling the state at record j exactly as the reference does.
+// Layout: S^T puts query row (lane % 16) in the lane and keys
+// 16*blk + 4*(lane/16) + r in its registers -- which is exactly the B-operand
+// layout of P^T for the PV product, so P never moves between the two MFMAs.
+// One workgroup = one chunk, one head, 64 query rows (4 waves x 16 rows).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int score_of(int dot, int mult) {
     int du = sra_rne32(dot, 2);                             // Q_SHIFT
     return sra_rne64((long long)du * (long long)mult, 15);  // attention.rs:233-239
 }
 
-__global__ __launch_bounds__(64) void k_attention(AttnArgs a) {
+constexpr int KLD = 80;  // LDS row stride (bytes) of the K tile and the V^T tile
+constexpr unsigned NOSEG = 0xFFFFu;
+
+__device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
+
+__device__ __forceinline__ int pack_limb(const unsigned* w, int shift, unsigned mask) {
+    return (int)(((w[0] >> shift) & mask) | (((w[1] >> shift) & mask) << 8) | (((w[2] >> shift) & mask) << 16) |
+                 (((w[3] >> shift) & mask) << 24));
+}
+
+__device__ __forceinline__ void rescale(unsigned long long& S, unsigned* vacc, unsigned e) {
+    S = (S * e + 0x8000ull) >> 16;
+    for (int i = 0; i < 16; i++) {
+        long long pr = (long long)(int)vacc[i] * (long long)e;
+        pr += pr >= 0 ? (1ll << 15) : -(1ll << 15);
+        vacc[i] = (unsigned)(int)(pr >> 16);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     __shared__ uint16_t lut[256];
-    __shared__ __attribute__((aligned(16))) int8_t qs[64];
-    __shared__ int sc[64];
-    const int lane = threadIdx.x;
-    const int row = blockIdx.x, h = blockIdx.y;
-    const int b = row / a.T, p = row % a.T;
-    for (int i = lane; i < 256; i += 64) lut[i] = a.lut[i];
-    if (p >= a.lens[b]) return;
+    __shared__ __attribute__((aligned(16))) int8_t Ks[64 * KLD];
+    __shared__ __attribute__((aligned(16))) int8_t Vt[64 * KLD];
+    __shared__ __attribute__((aligned(16))) unsigned scw[4][16][64];  // scores, then (w | seg << 16)
+    __shared__ unsigned rec_e[4][16][64];                            // rescale factor of record j (0 = none)
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int row = lane & 15, grp = lane >> 4;
+    const int q0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
+    const int T = a.T, len = a.lens[b];
+    if (q0 >= len) return;
+    for (int i = tid; i < 256; i += 256) lut[i] = a.lut[i];
     const int D = a.H * 64;
-    qs[lane] = a.q[(size_t)row * D + h * 64 + lane];
-    __syncthreads();
     const int g = a.kv_mode == 1 ? (h * a.G) / a.H : 0;
-    const int8_t* K = a.kc + ((size_t)b * a.KH + g) * a.T * 64;
-    const int8_t* V = a.vc + ((size_t)b * a.KH + g) * a.T * 64;
+    const int8_t* Kg = a.kc + ((size_t)b * a.KH + g) * T * 64;
+    const int8_t* Vg = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP;
     const int mult = a.score_mult[h];
-    const int* q4 = (const int*)qs;
+    const int p = q0 + wave * 16 + row;  // this lane's query position
+    const int wrow0 = q0 + wave * 16;
+    const bool wave_live = wrow0 < len;
+    const int wave_last = min(wrow0 + 15, len - 1);
+
+    v4i qop = (v4i){0, 0, 0, 0};
+    if (p < T) qop = *(const v4i*)(a.q + ((size_t)b * T + p) * D + h * 64 + grp * 16);
 
     int m = INT32_MIN;
     unsigned long long S = 0;
-    unsigned vacc = 0;
-    if (a.sink) {  // attention.rs:211-224
+    unsigned vacc[16];
+    for (int i = 0; i < 16; i++) vacc[i] = 0;
+    if (a.sink) {  // attention.rs:211-224: the sink key's score is the initial max, weight E(0)
+        const int* sk = (const int*)(a.sink + grp * 16);
         int dot = 0;
-        for (int i = 0; i < 64; i++) dot += (int)qs[i] * (int)a.sink[i];
+        for (int i = 0; i < 4; i++) dot = __builtin_amdgcn_sdot4(qop[i], sk[i], dot, false);
+        dot += __shfl_xor(dot, 16, 64);
+        dot += __shfl_xor(dot, 32, 64);
         m = score_of(dot, mult);
         S = 65535ull;
     }
-    for (int t0 = 0; t0 <= p; t0 += 64) {
-        const int t = t0 + lane;
-        int s = 0;
-        if (t <= p) {
-            const int* k4 = (const int*)(K + (size_t)t * 64);
-            int dot = 0;
-            for (int i = 0; i < 16; i++) dot = __builtin_amdgcn_sdot4(q4[i], k4[i], dot, false);
-            s = score_of(dot, mult);
-        }
-        sc[lane] = s;
+
+    const int ntiles = (min(q0 + 63, len - 1)) / 64 + 1;
+    for (int kt = 0; kt < ntiles; kt++) {
+        const int t0 = kt * 64;
         __syncthreads();
-        const int nt = min(64, p - t0 + 1);
-        for (int j = 0; j < nt; j++) {
-            const int sj = sc[j];
-            if (sj > m) {
-                if (m != INT32_MIN) {
-                    unsigned e = exp_q16((int)((unsigned)m - (unsigned)sj), lut, a.coef);
-                    S = (S * e + 0x8000ull) >> 16;
-                    long long pr = (long long)(int)vacc * (long long)e;
-                    pr += pr >= 0 ? (1ll << 15) : -(1ll << 15);
-                    vacc = (unsigned)(int)(pr >> 16);
+        {
+            const int r = tid >> 2, c = (tid & 3) * 16;
+            int4 kv = make_int4(0, 0, 0, 0);
+            if (t0 + r < T) kv = *(const int4*)(Kg + (size_t)(t0 + r) * 64 + c);
+            *(int4*)(Ks + r * KLD + c) = kv;
+            *(int4*)(Vt + r * KLD + c) = *(const int4*)(Vg + (size_t)r * a.TP + t0 + c);
+        }
+        __syncthreads();
+        if (!wave_live || t0 > wave_last) continue;
+
+        // 1. S^T = K Q^T, score epilogue, store row-major [row][key]
+        for (int blk = 0; blk < 4; blk++) {
+            v4i kop = *(const v4i*)(Ks + (blk * 16 + row) * KLD + grp * 16);
+            v4i st = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, qop, (v4i){0, 0, 0, 0}, 0, 0, 0);
+            int4 sv;
+            sv.x = score_of(st[0], mult);
+            sv.y = score_of(st[1], mult);
+            sv.z = score_of(st[2], mult);
+            sv.w = score_of(st[3], mult);
+            *(int4*)&scw[wave][row][blk * 16 + grp * 4] = sv;
+        }
+        wave_lds_fence();
+
+        // 2. in-order scan of keys [16*grp, 16*grp+16) of this row
+        int sv[16];
+        for (int i = 0; i < 4; i++) {
+            int4 v = *(const int4*)&scw[wave][row][grp * 16 + i * 4];
+            sv[i * 4] = v.x; sv[i * 4 + 1] = v.y; sv[i * 4 + 2] = v.z; sv[i * 4 + 3] = v.w;
+        }
+        const int kbase = t0 + grp * 16;
+        int nvalid = p - kbase + 1;  // keys t <= p are visible (causal)
+        nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
+        int bmax = INT32_MIN;
+        for (int k = 0; k < 16; k++)
+            if (k < nvalid) bmax = max(bmax, sv[k]);
+        // exclusive running max from the lanes holding earlier keys of the row
+        int e1 = __shfl(bmax, (lane - 16) & 63, 64), e2 = __shfl(bmax, (lane - 32) & 63, 64),
+            e3 = __shfl(bmax, (lane - 48) & 63, 64);
+        int cur = m;
+        if (grp >= 1) cur = max(cur, e1);
+        if (grp >= 2) cur = max(cur, e2);
+        if (grp >= 3) cur = max(cur, e3);
+        int nrec = 0;
+        for (int k = 0; k < 16; k++)
+            if (k < nvalid && sv[k] > cur) { nrec++; cur = sv[k]; }
+        int r1 = __shfl(nrec, (lane - 16) & 63, 64), r2 = __shfl(nrec, (lane - 32) & 63, 64),
+            r3 = __shfl(nrec, (lane - 48) & 63, 64);
+        int seg = 0;
+        if (grp >= 1) seg += r1;
+        if (grp >= 2) seg += r2;
+        if (grp >= 3) seg += r3;
+        // replay with weights
+        cur = m;
+        if (grp >= 1) cur = max(cur, e1);
+        if (grp >= 2) cur = max(cur, e2);
+        if (grp >= 3) cur = max(cur, e3);
+        unsigned wsg[16];
+        for (int k = 0; k < 16; k++) {
+            if (k < nvalid) {
+                const int s = sv[k];
+                if (s > cur) {
+                    unsigned e = cur != INT32_MIN ? exp_q16((int)((unsigned)cur - (unsigned)s), lut, 378194u) : 0u;
+                    rec_e[wave][row][seg] = e;
+                    seg++;
+                    cur = s;
                 }
-                m = sj;
+                unsigned w = exp_q16((int)((unsigned)s - (unsigned)cur), lut, 378194u);
+                wsg[k] = w | ((unsigned)seg << 16);
+            } else {
+                wsg[k] = NOSEG << 16;
             }
-            unsigned w = exp_q16((int)((unsigned)sj - (unsigned)m), lut, a.coef);
-            S += w;
-            vacc += (unsigned)((int)w * (int)V[(size_t)(t0 + j) * 64 + lane]);
         }
-        __syncthreads();
+        for (int i = 0; i < 4; i++)
+            *(uint4*)&scw[wave][row][grp * 16 + i * 4] = make_uint4(wsg[i * 4], wsg[i * 4 + 1], wsg[i * 4 + 2], wsg[i * 4 + 3]);
+        // row-wide results: new running max and record count
+        int mrow = cur;
+        mrow = max(mrow, __shfl_xor(mrow, 16, 64));
+        mrow = max(mrow, __shfl_xor(mrow, 32, 64));
+        int nrow = nrec + __shfl_xor(nrec, 16, 64);
+        nrow += __shfl_xor(nrow, 32, 64);
+        int nmax = nrow;
+        for (int o = 1; o < 16; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
+        m = mrow;
+        wave_lds_fence();
+
+        // 3. PV per segment. P^T operand: this lane's keys 16*blk + 4*grp + r (r fastest).
+        unsigned wk[16];
+        for (int blk = 0; blk < 4; blk++) {
+            uint4 v = *(const uint4*)&scw[wave][row][blk * 16 + grp * 4];
+            wk[blk * 4] = v.x; wk[blk * 4 + 1] = v.y; wk[blk * 4 + 2] = v.z; wk[blk * 4 + 3] = v.w;
+        }
+        v4i vop[4];
+        for (int db = 0; db < 4; db++) {
+            const int8_t* vr = Vt + (db * 16 + row) * KLD + grp * 4;
+            vop[db] = (v4i){*(const int*)(vr), *(const int*)(vr + 16), *(const int*)(vr + 32), *(const int*)(vr + 48)};
+        }
+        for (int j = 0; j <= nmax; j++) {
+            unsigned wj[16];
+            unsigned sj = 0;
+            for (int k = 0; k < 16; k++) {
+                wj[k] = (wk[k] >> 16) == (unsigned)j ? (wk[k] & 0xFFFFu) : 0u;
+                sj += wj[k];
+            }
+            v4i bc, bb, ba;
+            for (int blk = 0; blk < 4; blk++) {
+                bc[blk] = pack_limb(wj + blk * 4, 0, 127u);
+                bb[blk] = pack_limb(wj + blk * 4, 7, 127u);
+                ba[blk] = pack_limb(wj + blk * 4, 14, 3u);
+            }
+            sj += __shfl_xor(sj, 16, 64);
+            sj += __shfl_xor(sj, 32, 64);
+            if (j >= 1 && j <= nrow) {
+                unsigned e = rec_e[wave][row][j - 1];
+                if (e) rescale(S, vacc, e);
+            }
+            S += sj;
+            for (int db = 0; db < 4; db++) {
+                v4i z = (v4i){0, 0, 0, 0};
+                v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[db], bc, z, 0, 0, 0);
+                v4i cb = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[db], bb, z, 0, 0, 0);
+                v4i ca = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[db], ba, z, 0, 0, 0);
+                for (int r = 0; r < 4; r++)
+                    vacc[db * 4 + r] += ((unsigned)ca[r] << 14) + ((unsigned)cb[r] << 7) + (unsigned)cc[r];
+            }
+        }
     }
-    unsigned long long den = S == 0 ? 1ull : S;
-    a.out[(size_t)row * D + h * 64 + lane] = (int8_t)clamp127(div_rne_s32_u64((int)vacc, den));
+    if (p >= len) return;
+    // normalize (attention.rs:278-285); lane holds dims 16*db + 4*grp + r
+    const unsigned long long den = S == 0 ? 1ull : S;
+    int8_t* o = a.out + ((size_t)b * T + p) * D + h * 64 + grp * 4;
+    for (int db = 0; db < 4; db++) {
+        unsigned pk = 0;
+        for (int r = 0; r < 4; r++)
+            pk |= ((unsigned)(uint8_t)(int8_t)clamp127(div_rne_s32_u64((int)vacc[db * 4 + r], den))) << (8 * r);
+        *(unsigned*)(o + db * 16) = pk;
+    }
 }
 
-void launch_attention(const AttnArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_attention, dim3((unsigned)a.M, (unsigned)a.H), dim3(64), 0, s, a);
+void launch_attention(const AttnArgs& a, int B, hipStream_t s) {
+    dim3 grid((unsigned)((a.T + 63) / 64), (unsigned)a.H, (unsigned)B);
+    hipLaunchKernelGGL(k_attention, grid, dim3(256), 0, s, a);
 }
 
 // ---------------------------------------------------------------------------
