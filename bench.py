@@ -91,6 +91,7 @@ def main():
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--tokens", type=int, default=0, help="truncate the workload (profiling runs only)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); chunks shard across GPUs with no "
@@ -106,6 +107,8 @@ def main():
     weights = czip_amd.ModelWeights(model_path, kv_mode)
     cfg = weights.config
     tokens = make_tokens(wl, model_path, cfg["vocab_size"])
+    if args.tokens:
+        tokens = tokens[:args.tokens]
     chunk = wl["chunk"]
     n = int(tokens.size)
     log(f"workload {args.workload}: {n} tokens, chunk {chunk}")

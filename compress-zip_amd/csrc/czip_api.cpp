@@ -68,8 +68,9 @@ struct czip_job {
     int32_t* out_lens = nullptr;
     int32_t* err = nullptr;
     // per sub-batch scratch
-    uint32_t *inp = nullptr, *tgt = nullptr, *lohi = nullptr;
-    int32_t* lens = nullptr;
+    uint32_t *inp = nullptr, *tgt = nullptr, *lohi = nullptr, *lohi_all = nullptr;
+    int32_t* lens = nullptr;      // lengths of the chunks of the current sub-batch
+    int32_t* lens_all = nullptr;  // lengths of every chunk of the job
     int32_t* x = nullptr;
     int8_t *xn = nullptr, *q8 = nullptr, *kc = nullptr, *vc = nullptr, *attn = nullptr, *y8 = nullptr, *r8 = nullptr;
     int32_t* logits = nullptr;
@@ -322,8 +323,6 @@ czip_status alloc_scratch(czip_ctx* c, czip_job* j, int BC, int T) {
     czip_status rc;
     if ((rc = dalloc(c, j->allocs, &j->inp, M))) return rc;
     if ((rc = dalloc(c, j->allocs, &j->tgt, M))) return rc;
-    if ((rc = dalloc(c, j->allocs, &j->lohi, 2 * M))) return rc;
-    if ((rc = dalloc(c, j->allocs, &j->lens, (size_t)BC))) return rc;
     if ((rc = dalloc(c, j->allocs, &j->x, M * d))) return rc;
     if ((rc = dalloc(c, j->allocs, &j->xn, M * d))) return rc;
     if ((rc = dalloc(c, j->allocs, &j->q8, M * d))) return rc;
@@ -426,6 +425,8 @@ czip_status run_rows(czip_ctx* c, const uint32_t* rows_in, const uint32_t* rows_
     const int V = c->cfg.vocab;
     uint32_t* dcum = nullptr;
     if (mode == 2 && (rc = dalloc(c, j.allocs, &dcum, (size_t)BC * T * V))) { free_job_mem(&j); return rc; }
+    if ((rc = dalloc(c, j.allocs, &j.lohi, (size_t)BC * T * 2))) { free_job_mem(&j); return rc; }
+    if ((rc = dalloc(c, j.allocs, &j.lens, (size_t)BC))) { free_job_mem(&j); return rc; }
     for (int b0 = 0; b0 < B && rc == 0; b0 += BC) {
         const int nb = std::min(BC, B - b0);
         const size_t M = (size_t)nb * T;
@@ -438,10 +439,10 @@ czip_status run_rows(czip_ctx* c, const uint32_t* rows_in, const uint32_t* rows_
         if (mode == 0) {
             e = hipMemcpyAsync((int32_t*)host_out + (size_t)b0 * T * V, j.logits, M * V * 4, hipMemcpyDeviceToHost, c->stream);
         } else if (mode == 1) {
-            { Timed t(c, "cdf"); launch_cdf(j.logits, (int)M, V, j.tgt, j.lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 0, j.lohi, c->stream); }
+            { Timed t(c, "cdf"); launch_cdf(j.logits, (int)M, V, j.tgt, j.lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 0, j.lohi, 0, c->stream); }
             e = hipMemcpyAsync((uint32_t*)host_out + (size_t)b0 * T * 2, j.lohi, M * 8, hipMemcpyDeviceToHost, c->stream);
         } else {
-            { Timed t(c, "cdf"); launch_cdf(j.logits, (int)M, V, nullptr, j.lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 1, dcum, c->stream); }
+            { Timed t(c, "cdf"); launch_cdf(j.logits, (int)M, V, nullptr, j.lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 1, dcum, 0, c->stream); }
             e = hipMemcpyAsync((uint32_t*)host_out + (size_t)b0 * T * V, dcum, M * V * 4, hipMemcpyDeviceToHost, c->stream);
         }
         if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
@@ -531,6 +532,9 @@ extern "C" czip_status czip_compress_plan(czip_ctx* c, const uint32_t* tokens, i
     if ((rc = dalloc(c, j->allocs, &j->out, (size_t)(nch * j->slot)))) { free_job_mem(j.get()); return rc; }
     if ((rc = dalloc(c, j->allocs, &j->out_lens, (size_t)nch))) { free_job_mem(j.get()); return rc; }
     if ((rc = dalloc(c, j->allocs, &j->err, 1))) { free_job_mem(j.get()); return rc; }
+    // coder intervals and lengths of every chunk, so one encoder launch covers all chunks
+    if ((rc = dalloc(c, j->allocs, &j->lohi_all, (size_t)(nch * chunk * 2)))) { free_job_mem(j.get()); return rc; }
+    if ((rc = dalloc(c, j->allocs, &j->lens_all, (size_t)nch))) { free_job_mem(j.get()); return rc; }
     if ((rc = alloc_scratch(c, j.get(), j->BC, chunk))) { free_job_mem(j.get()); return rc; }
     if (n > 0) {
         hipError_t e = hipMemcpy(j->tok, tokens, (size_t)n * 4, hipMemcpyHostToDevice);
@@ -550,11 +554,16 @@ static czip_status run_compress(czip_job* j) {
     for (int64_t c0 = 0; c0 < j->nchunks; c0 += j->BC) {
         const int nb = (int)std::min<int64_t>(j->BC, j->nchunks - c0);
         const int M = nb * T;
+        j->lens = j->lens_all + c0;
         { Timed t(c, "prep"); launch_prep_chunks(j->tok, j->n_tokens, c0, nb, T, j->inp, j->tgt, j->lens, s); }
         czip_status rc = forward_batch(c, j, nb, T);
         if (rc) return rc;
-        { Timed t(c, "cdf"); launch_cdf(j->logits, M, V, j->tgt, j->lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 0, j->lohi, s); }
-        { Timed t(c, "encode"); launch_encode(j->lohi, j->lens, nb, T, c->cfg.target_total, j->out + c0 * j->slot, j->slot, j->out_lens + c0, j->err, s); }
+        { Timed t(c, "cdf"); launch_cdf(j->logits, M, V, j->tgt, j->lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 0, j->lohi_all, c0 * T, s); }
+    }
+    if (j->nchunks > 0) {
+        Timed t(c, "encode");
+        launch_encode(j->lohi_all, j->lens_all, (int)j->nchunks, T, c->cfg.target_total, j->out, j->slot, j->out_lens,
+                      j->err, s);
     }
     HIPCHECK(c, hipGetLastError());
     HIPCHECK(c, hipStreamSynchronize(s));

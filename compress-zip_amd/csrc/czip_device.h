@@ -1,0 +1,155 @@
+// Device-side integer primitives shared by the gfx950 kernels.
+//
+// Bit-exact copies of rust/src/primitives.rs, lut.rs and rmsnorm.rs.
+// Wrapping i32 arithmetic is written with unsigned types (the reference is
+// built without overflow checks, so i32 adds and multiplies wrap).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace czip {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr unsigned ATTN_COEF_Q24 = 378194u;  // (LOG2E / 64 * 2^24 + 0.5) as u32, attention.rs:17-19
+constexpr uint32_t BOS_TOKEN = 1022u;        // main.rs:222, 387
+
+__device__ __forceinline__ int clamp127(int x) { return x < -127 ? -127 : (x > 127 ? 127 : x); }
+
+// primitives.rs:18-42
+__device__ __forceinline__ int sra_rne32(int v, unsigned sh) {
+    if (sh == 0) return v;
+    unsigned sign = (unsigned)(v >> 31);
+    unsigned av = ((unsigned)v ^ sign) - sign;
+    unsigned q = av >> sh;
+    unsigned r = av & ((1u << sh) - 1u);
+    unsigned half = 1u << (sh - 1);
+    q += (r > half) ? 1u : ((r == half) ? (q & 1u) : 0u);
+    return (int)((q ^ sign) - sign);
+}
+
+// primitives.rs:49-73
+__device__ __forceinline__ int sra_rne64(long long v, unsigned sh) {
+    if (sh == 0) return (int)(v < INT32_MIN ? INT32_MIN : (v > INT32_MAX ? INT32_MAX : v));
+    unsigned long long sign = (unsigned long long)(v >> 63);
+    unsigned long long av = ((unsigned long long)v ^ sign) - sign;
+    unsigned long long q = av >> sh;
+    unsigned long long r = av & ((1ull << sh) - 1ull);
+    unsigned long long half = 1ull << (sh - 1);
+    q += (r > half) ? 1ull : ((r == half) ? (q & 1ull) : 0ull);
+    long long so = (long long)((q ^ sign) - sign);
+    return (int)(so < INT32_MIN ? INT32_MIN : (so > INT32_MAX ? INT32_MAX : so));
+}
+
+// sra_rne64((i64)a * b, sh) computed in sign-magnitude form with one
+// 32x32->64 multiply; identical results for every (a, b, sh in 1..31).
+__device__ __forceinline__ int mul_sra_rne(int a, int b, unsigned sh) {
+    const unsigned sa = (unsigned)(a >> 31), sb = (unsigned)(b >> 31);
+    const unsigned ua = ((unsigned)a ^ sa) - sa, ub = ((unsigned)b ^ sb) - sb;
+    const unsigned long long p = (unsigned long long)ua * ub;
+    unsigned long long q = p >> sh;
+    const unsigned r = (unsigned)p & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    q += (r > half) ? 1ull : ((r == half) ? (q & 1ull) : 0ull);
+    const bool neg = (sa ^ sb) != 0u && p != 0ull;
+    if (neg) return q >= 0x80000000ull ? INT32_MIN : -(int)q;
+    return q > 0x7FFFFFFFull ? INT32_MAX : (int)q;
+}
+
+// model.rs:280-300
+__device__ __forceinline__ int requant(int v, int mult, int shift) {
+    if (shift <= 0) {
+        long long p = (long long)v * (long long)mult;
+        return (int)(p < -127 ? -127 : (p > 127 ? 127 : p));
+    }
+    if (shift < 32) return clamp127(mul_sra_rne(v, mult, (unsigned)shift));
+    return clamp127(sra_rne64((long long)v * (long long)mult, (unsigned)shift));
+}
+
+// primitives.rs:80-97
+__device__ __forceinline__ unsigned udiv_rne(unsigned n, unsigned d) {
+    if (d == 0) return 0;
+    unsigned q = n / d;
+    unsigned r = n - q * d;
+    unsigned tr = r << 1;
+    return tr > d ? q + 1 : (tr == d ? q + (q & 1u) : q);
+}
+
+// primitives.rs:192-213
+__device__ __forceinline__ unsigned isqrt32(unsigned x) {
+    unsigned op = x, res = 0, one = 1u << 30;
+    while (one > op) one >>= 2;
+    while (one != 0) {
+        if (op >= res + one) { op -= res + one; res = (res >> 1) + one; }
+        else res >>= 1;
+        one >>= 2;
+    }
+    return res;
+}
+
+// rmsnorm.rs:14-30
+__device__ __forceinline__ int inv_rms_q15(int mean_sq) {
+    unsigned ms = mean_sq > 0 ? (unsigned)mean_sq : 1u;
+    unsigned inv = udiv_rne(8388608u, isqrt32(ms << 16));
+    return (int)(inv < 1u ? 1u : (inv > 32768u ? 32768u : inv));
+}
+
+// lut.rs:213-235 / softmax_cdf.rs:55-77
+__device__ __forceinline__ unsigned exp_q16(int diff, const uint16_t* lut, unsigned coef) {
+    if (diff >= 0) return 65535u;
+    unsigned neg = 0u - (unsigned)diff;
+    unsigned t = (unsigned)(((unsigned long long)neg * coef + (1ull << 23)) >> 24);
+    unsigned ip = t >> 8;
+    if (ip >= 31u) return 1u;
+    unsigned out = ((65536u >> ip) * (unsigned)lut[t & 255u] + 0x8000u) >> 16;
+    return out < 1u ? 1u : (out > 65535u ? 65535u : out);
+}
+
+// primitives.rs:163-185 (the result is formed with i32 wrap like `as i32 * sign`)
+__device__ __forceinline__ int div_rne_s32_u64(int num, unsigned long long den) {
+    if (den == 0) return 0;
+    unsigned long long an = (unsigned long long)(num < 0 ? 0u - (unsigned)num : (unsigned)num);
+    unsigned long long q, r;
+    if (den <= 0xFFFFFFFFull) {
+        unsigned q32 = (unsigned)an / (unsigned)den;
+        q = q32;
+        r = an - q * den;
+    } else {
+        q = 0;
+        r = an;
+    }
+    unsigned long long tr = r << 1;
+    unsigned long long rq = tr > den ? q + 1 : (tr == den ? q + (q & 1ull) : q);
+    unsigned u = (unsigned)rq;
+    return (int)(num < 0 ? 0u - u : u);
+}
+
+// floor(a / d) for a < 2^62, 0 < d < 2^32, via an f64 estimate and an exact
+// integer correction (the estimate is within one of the true quotient).
+__device__ __forceinline__ unsigned long long udiv64_32(unsigned long long a, unsigned d, double inv_d) {
+    unsigned long long q = (unsigned long long)((double)a * inv_d);
+    long long r = (long long)(a - q * (unsigned long long)d);
+    while (r < 0) { q -= 1; r += (long long)d; }
+    while (r >= (long long)d) { q += 1; r -= (long long)d; }
+    return q;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ unsigned wave_sum_u(unsigned v) {
+    for (int o = 32; o > 0; o >>= 1) v += (unsigned)__shfl_xor((int)v, o, 64);
+    return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+}  // namespace czip

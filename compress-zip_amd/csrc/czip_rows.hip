@@ -1,0 +1,394 @@
+// Row-wise kernels: chunk preparation, embedding + RMSNorm, residual + RMSNorm,
+// logits -> cumulative frequencies, and the arithmetic encoder.
+#include "czip_device.h"
+#include "czip_kernels.h"
+
+namespace czip {
+
+// ---------------------------------------------------------------------------
+// Chunk preparation: inputs [BOS, t0..t_{n-2}] and targets per chunk
+// (main.rs:209-226).  Padding rows get token 0 and are never read back.
+// ---------------------------------------------------------------------------
+__global__ void k_prep_chunks(const uint32_t* __restrict__ toks, long long n, long long chunk0, int nb, int T,
+                              uint32_t* __restrict__ inp, uint32_t* __restrict__ tgt, int32_t* __restrict__ lens) {
+    long long row = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= (long long)nb * T) return;
+    int b = (int)(row / T), p = (int)(row % T);
+    long long start = (chunk0 + b) * (long long)T;
+    long long len = n - start;
+    if (len > T) len = T;
+    if (len < 0) len = 0;
+    if (p == 0) lens[b] = (int32_t)len;
+    if (p < len) {
+        inp[row] = p == 0 ? BOS_TOKEN : toks[start + p - 1];
+        tgt[row] = toks[start + p];
+    } else {
+        inp[row] = 0u;
+        tgt[row] = 0u;
+    }
+}
+
+void launch_prep_chunks(const uint32_t* toks, int64_t n, int64_t chunk0, int nb, int T, uint32_t* inp,
+                        uint32_t* tgt, int32_t* lens, hipStream_t s) {
+    long long rows = (long long)nb * T;
+    hipLaunchKernelGGL(k_prep_chunks, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, toks, (long long)n,
+                       (long long)chunk0, nb, T, inp, tgt, lens);
+}
+
+// ---------------------------------------------------------------------------
+// Row kernels: one wavefront per token row, d <= 1024.  Lane l owns the
+// 4-element groups g = l, l + 64, ... (elements 4g .. 4g+3), so loads and
+// stores are 4-byte (int8) or 16-byte (int32) vectors.
+// ---------------------------------------------------------------------------
+constexpr int RG = 4;  // groups per lane: d <= 64 * 4 * RG
+
+struct RowI8 {
+    int v[RG][4];
+};
+
+__device__ __forceinline__ void unpack4(unsigned w, int* o) {
+    o[0] = (int)(int8_t)(w & 0xFF);
+    o[1] = (int)(int8_t)((w >> 8) & 0xFF);
+    o[2] = (int)(int8_t)((w >> 16) & 0xFF);
+    o[3] = (int)(int8_t)(w >> 24);
+}
+__device__ __forceinline__ unsigned pack4(const int* v) {
+    return ((unsigned)(uint8_t)(int8_t)v[0]) | ((unsigned)(uint8_t)(int8_t)v[1] << 8) |
+           ((unsigned)(uint8_t)(int8_t)v[2] << 16) | ((unsigned)(uint8_t)(int8_t)v[3] << 24);
+}
+
+// rmsnorm.rs:40-75 on the wave-distributed row: y = clamp(sra_rne((x*w)*inv, 15))
+__device__ __forceinline__ void rms_row(const RowI8& x, const int8_t* __restrict__ w, int d, int lane, RowI8& y) {
+    const int ng = d >> 2;
+    unsigned ss = 0;
+#pragma unroll
+    for (int j = 0; j < RG; j++)
+        if (lane + 64 * j < ng)
+#pragma unroll
+            for (int k = 0; k < 4; k++) ss += (unsigned)(x.v[j][k] * x.v[j][k]);
+    ss = wave_sum_u(ss);
+    int mean_sq = (int)(ss / (unsigned)d) + 1;  // eps_scaled = 1 (rmsnorm.rs:80-83)
+    if (mean_sq < 1) mean_sq = 1;
+    const int inv = inv_rms_q15(mean_sq);
+#pragma unroll
+    for (int j = 0; j < RG; j++) {
+        const int g = lane + 64 * j;
+        if (g < ng) {
+            int wv[4];
+            unpack4(*(const unsigned*)(w + 4 * g), wv);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                int tmp = (int)((unsigned)(x.v[j][k] * wv[k]) * (unsigned)inv);
+                y.v[j][k] = clamp127(sra_rne32(tmp, 15));
+            }
+        }
+    }
+}
+
+// x = E[tok] (model.rs:372-374); xn = rmsnorm(clamp(x), w) (model.rs:384-385)
+__global__ __launch_bounds__(256) void k_embed_norm(const uint32_t* __restrict__ inp, const int8_t* __restrict__ embed,
+                                                    const int8_t* __restrict__ w, int M, int d,
+                                                    int32_t* __restrict__ x, int8_t* __restrict__ xn) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    const int ng = d >> 2;
+    const int8_t* e = embed + (size_t)inp[row] * d;
+    RowI8 xi, y;
+#pragma unroll
+    for (int j = 0; j < RG; j++) {
+        const int g = lane + 64 * j;
+        if (g < ng) {
+            unpack4(*(const unsigned*)(e + 4 * g), xi.v[j]);
+            *(int4*)(x + (size_t)row * d + 4 * g) = make_int4(xi.v[j][0], xi.v[j][1], xi.v[j][2], xi.v[j][3]);
+#pragma unroll
+            for (int k = 0; k < 4; k++) xi.v[j][k] = clamp127(xi.v[j][k]);
+        }
+    }
+    rms_row(xi, w, d, lane, y);
+#pragma unroll
+    for (int j = 0; j < RG; j++) {
+        const int g = lane + 64 * j;
+        if (g < ng) *(unsigned*)(xn + (size_t)row * d + 4 * g) = pack4(y.v[j]);
+    }
+}
+
+void launch_embed_norm(const uint32_t* inp, const int8_t* embed, const int8_t* w, int M, int d, int32_t* x,
+                       int8_t* xn, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed_norm, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, s, inp, embed, w, M, d, x, xn);
+}
+
+// x += rmsnorm(y8, w1) (model.rs:429-434 / 463-468);
+// xn = rmsnorm(clamp(x), w2) (model.rs:438-439, next layer 384-385, final 473-474)
+__global__ __launch_bounds__(256) void k_resid_norm(int32_t* __restrict__ x, const int8_t* __restrict__ y8,
+                                                    const int8_t* __restrict__ w1, const int8_t* __restrict__ w2,
+                                                    int M, int d, int8_t* __restrict__ xn) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    const int ng = d >> 2;
+    RowI8 yi, yn, xi;
+#pragma unroll
+    for (int j = 0; j < RG; j++) {
+        const int g = lane + 64 * j;
+        if (g < ng) unpack4(*(const unsigned*)(y8 + (size_t)row * d + 4 * g), yi.v[j]);
+    }
+    rms_row(yi, w1, d, lane, yn);
+#pragma unroll
+    for (int j = 0; j < RG; j++) {
+        const int g = lane + 64 * j;
+        if (g < ng) {
+            int4* px = (int4*)(x + (size_t)row * d + 4 * g);
+            int4 xv = *px;
+            int nv[4] = {(int)((unsigned)xv.x + (unsigned)yn.v[j][0]), (int)((unsigned)xv.y + (unsigned)yn.v[j][1]),
+                         (int)((unsigned)xv.z + (unsigned)yn.v[j][2]), (int)((unsigned)xv.w + (unsigned)yn.v[j][3])};
+            *px = make_int4(nv[0], nv[1], nv[2], nv[3]);
+#pragma unroll
+            for (int k = 0; k < 4; k++) xi.v[j][k] = clamp127(nv[k]);
+        }
+    }
+    rms_row(xi, w2, d, lane, yn);
+#pragma unroll
+    for (int j = 0; j < RG; j++) {
+        const int g = lane + 64 * j;
+        if (g < ng) *(unsigned*)(xn + (size_t)row * d + 4 * g) = pack4(yn.v[j]);
+    }
+}
+
+void launch_resid_norm(int32_t* x, const int8_t* y8, const int8_t* w1, const int8_t* w2, int M, int d, int8_t* xn,
+                       hipStream_t s) {
+    hipLaunchKernelGGL(k_resid_norm, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, s, x, y8, w1, w2, M, d, xn);
+}
+
+// ---------------------------------------------------------------------------
+// Logits -> cumulative frequencies (softmax_cdf.rs:85-139).
+// WPR wavefronts per row, EPL consecutive logits per lane (V <= 64*WPR*EPL).
+// The frequency f = 1 + floor(e * R / S) (R = total - V) is formed exactly as
+// f = 1 + e*Q + floor(e*Rm / S) with Q = R / S, Rm = R % S: e*Q < 2^31
+// because S >= 65535 (the max logit weighs 65535), and the small quotient is
+// an f32 estimate corrected by one exact 64-bit remainder test.
+// mode 0: write (cum_lo, cum_hi) of the row's target; mode 1: write the full
+// inclusive table.
+// ---------------------------------------------------------------------------
+template <int WPR, int EPL>
+__global__ __launch_bounds__(64 * WPR) void k_cdf(const int32_t* __restrict__ logits, int V,
+                                                  const uint32_t* __restrict__ targets,
+                                                  const int32_t* __restrict__ lens, int T,
+                                                  const uint16_t* __restrict__ glut, unsigned coef, unsigned total,
+                                                  int mode, uint32_t* __restrict__ out, long long out_row0) {
+    __shared__ uint16_t lut[256];
+    __shared__ int red_i[WPR];
+    __shared__ unsigned red_u[WPR];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row = blockIdx.x;
+    for (int i = tid; i < 256; i += 64 * WPR) lut[i] = glut[i];
+    if (lens && (row % T) >= lens[row / T]) return;  // uniform per block
+    __syncthreads();
+    const int i0 = tid * EPL;
+    const int32_t* L = logits + (size_t)row * V;
+    int lv[EPL];
+    if (i0 + EPL <= V) {
+#pragma unroll
+        for (int k = 0; k < EPL; k += 4) {
+            int4 v = *(const int4*)(L + i0 + k);
+            lv[k] = v.x; lv[k + 1] = v.y; lv[k + 2] = v.z; lv[k + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < EPL; k++) lv[k] = (i0 + k < V) ? L[i0 + k] : INT32_MIN;
+    }
+    auto bmax = [&](int v) {
+        v = wave_max_i(v);
+        if (WPR == 1) return v;
+        if (lane == 0) red_i[wave] = v;
+        __syncthreads();
+        int r = red_i[0];
+        for (int w = 1; w < WPR; w++) r = max(r, red_i[w]);
+        __syncthreads();
+        return r;
+    };
+    auto bmin = [&](int v) {
+        v = wave_min_i(v);
+        if (WPR == 1) return v;
+        if (lane == 0) red_i[wave] = v;
+        __syncthreads();
+        int r = red_i[0];
+        for (int w = 1; w < WPR; w++) r = min(r, red_i[w]);
+        __syncthreads();
+        return r;
+    };
+    auto bsum = [&](unsigned v) {
+        v = wave_sum_u(v);
+        if (WPR == 1) return v;
+        if (lane == 0) red_u[wave] = v;
+        __syncthreads();
+        unsigned r = 0;
+        for (int w = 0; w < WPR; w++) r += red_u[w];
+        __syncthreads();
+        return r;
+    };
+    int mx = INT32_MIN;
+#pragma unroll
+    for (int k = 0; k < EPL; k++) mx = max(mx, lv[k]);
+    mx = bmax(mx);
+    int am = 0x7FFFFFFF;
+#pragma unroll
+    for (int k = EPL - 1; k >= 0; k--)
+        if (i0 + k < V && lv[k] == mx) am = i0 + k;
+    am = bmin(am);
+    unsigned e[EPL];
+    unsigned ls = 0;
+#pragma unroll
+    for (int k = 0; k < EPL; k++) {
+        e[k] = (i0 + k < V) ? exp_q16((int)((unsigned)lv[k] - (unsigned)mx), lut, coef) : 0u;
+        ls += e[k];
+    }
+    const unsigned S = bsum(ls);  // <= 8192 * 65535 < 2^32
+    const unsigned R = total - (unsigned)V;
+    const unsigned Q = R / S, Rm = R - Q * S;
+    const float rf = (float)Rm / (float)S;
+    unsigned fl = 0;
+#pragma unroll
+    for (int k = 0; k < EPL; k++) {
+        unsigned f = 0;
+        if (i0 + k < V) {
+            unsigned q = (unsigned)((float)e[k] * rf);
+            const unsigned long long t = (unsigned long long)e[k] * Rm, u = (unsigned long long)q * S;
+            if (t < u) q -= 1;
+            else if (t - u >= S) q += 1;
+            f = 1u + e[k] * Q + q;
+        }
+        e[k] = f;
+        fl += f;
+    }
+    const unsigned rem = total - bsum(fl);
+    if (mode == 0) {
+        const int tok = (int)targets[row];
+        unsigned lo = 0, ft = 0;
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            lo += (i0 + k < tok) ? e[k] : 0u;
+            ft += (i0 + k == tok) ? e[k] : 0u;
+        }
+        lo = bsum(lo);
+        ft = bsum(ft);
+        if (am < tok) lo += rem;
+        if (am == tok) ft += rem;
+        if (tid == 0) {
+            out[(size_t)(out_row0 + row) * 2] = lo;
+            out[(size_t)(out_row0 + row) * 2 + 1] = lo + ft;
+        }
+    } else {
+        // exclusive scan of lane sums across the row
+        unsigned incl = fl;
+        for (int o = 1; o < 64; o <<= 1) {
+            unsigned v = (unsigned)__shfl_up((int)incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        unsigned excl = incl - fl;
+        if (WPR > 1) {
+            if (lane == 63) red_u[wave] = incl;
+            __syncthreads();
+            for (int w = 0; w < wave; w++) excl += red_u[w];
+        }
+        unsigned run = excl + (am < i0 ? rem : 0u);
+        uint32_t* o = out + (size_t)(out_row0 + row) * V;
+#pragma unroll
+        for (int k = 0; k < EPL; k++) {
+            if (i0 + k < V) {
+                run += e[k] + (i0 + k == am ? rem : 0u);
+                o[i0 + k] = run;
+            }
+        }
+    }
+}
+
+void launch_cdf(const int32_t* logits, int M, int V, const uint32_t* targets, const int32_t* lens, int T,
+                const uint16_t* lut, unsigned coef, unsigned total, int mode, uint32_t* out, int64_t out_row0,
+                hipStream_t s) {
+    if (V <= 1024)
+        hipLaunchKernelGGL((k_cdf<1, 16>), dim3((unsigned)M), dim3(64), 0, s, logits, V, targets, lens, T, lut, coef,
+                           total, mode, out, (long long)out_row0);
+    else if (V <= 4096)
+        hipLaunchKernelGGL((k_cdf<4, 16>), dim3((unsigned)M), dim3(256), 0, s, logits, V, targets, lens, T, lut, coef,
+                           total, mode, out, (long long)out_row0);
+    else
+        hipLaunchKernelGGL((k_cdf<4, 32>), dim3((unsigned)M), dim3(256), 0, s, logits, V, targets, lens, T, lut, coef,
+                           total, mode, out, (long long)out_row0);
+}
+
+// ---------------------------------------------------------------------------
+// Arithmetic encoder (arith_coder.rs:26-136), one thread per chunk.
+// ---------------------------------------------------------------------------
+struct BitOut {
+    uint8_t* buf;
+    long long cap, len;
+    unsigned cur;
+    int bit_pos;
+    int overflow;
+    __device__ void bit(unsigned b) {
+        if (b) cur |= 1u << bit_pos;
+        if (--bit_pos < 0) {
+            if (len < cap) buf[len] = (uint8_t)cur;
+            else overflow = 1;
+            len++;
+            cur = 0;
+            bit_pos = 7;
+        }
+    }
+};
+
+__global__ __launch_bounds__(64) void k_encode(const uint32_t* __restrict__ lohi, const int32_t* __restrict__ lens,
+                                               int nb, int T, unsigned total, uint8_t* __restrict__ out,
+                                               long long slot, int32_t* __restrict__ out_lens,
+                                               int32_t* __restrict__ err) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= nb) return;
+    const unsigned long long MASK = 0xFFFFFFFFull, HALF = 1ull << 31, QUART = 1ull << 30;
+    unsigned long long low = 0, high = MASK;
+    unsigned underflow = 0;
+    BitOut o{out + (size_t)c * slot, slot, 0, 0u, 7, 0};
+    const double invT = 1.0 / (double)total;
+    const int n = lens[c];
+    const uint2* lh = (const uint2*)(lohi + (size_t)c * T * 2);
+    uint2 nxt = n > 0 ? lh[0] : make_uint2(0, 0);
+    for (int i = 0; i < n; i++) {
+        const uint2 cur = nxt;
+        if (i + 1 < n) nxt = lh[i + 1];  // prefetch the next interval
+        const unsigned long long range = high - low + 1;
+        high = low + udiv64_32((unsigned long long)cur.y * range, total, invT) - 1;
+        low = low + udiv64_32((unsigned long long)cur.x * range, total, invT);
+        for (;;) {
+            if (((low ^ high) & HALF) == 0) {
+                unsigned bitv = (unsigned)((low >> 31) & 1);
+                o.bit(bitv);
+                for (unsigned u = 0; u < underflow; u++) o.bit(bitv ^ 1u);
+                underflow = 0;
+                low = (low << 1) & MASK;
+                high = ((high << 1) & MASK) | 1;
+            } else if ((low & ~high & QUART) != 0) {
+                underflow += 1;
+                low = ((low << 1) ^ HALF) & MASK;
+                high = (((high ^ HALF) << 1) | HALF | 1) & MASK;
+            } else {
+                break;
+            }
+        }
+    }
+    o.bit(1u);  // finish(): terminating bit, then flush the partial byte
+    if (o.bit_pos < 7) {
+        if (o.len < o.cap) o.buf[o.len] = (uint8_t)o.cur;
+        else o.overflow = 1;
+        o.len++;
+    }
+    out_lens[c] = (int32_t)o.len;
+    if (o.overflow) atomicOr(err, 1);
+}
+
+void launch_encode(const uint32_t* lohi, const int32_t* lens, int nb, int T, unsigned total, uint8_t* out,
+                   int64_t slot, int32_t* out_lens, int32_t* err, hipStream_t s) {
+    hipLaunchKernelGGL(k_encode, dim3((unsigned)((nb + 63) / 64)), dim3(64), 0, s, lohi, lens, nb, T, total, out,
+                       (long long)slot, out_lens, err);
+}
+
+}  // namespace czip

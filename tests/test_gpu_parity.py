@@ -142,6 +142,25 @@ def test_compress_random_d512(amd, orc, random_models):
     assert got == ref
 
 
+@pytest.mark.parametrize("vocab", [2048, 8192])
+def test_cdf_large_vocab(amd, orc, tmp_path, vocab):
+    """The multi-wave CDF variants (V > 1024) against the oracle's tables and coded bytes."""
+    from czip_amd import synth
+    path = synth.write_random_model(str(tmp_path / f"v{vocab}.czm"), d=256, n_layers=1, n_heads=4, n_kv=1,
+                                    d_ff=256, vocab=vocab, ctx=128, seed=40 + vocab)
+    gm, om = _model_pair(amd, orc, path, amd.KV_RUST_COMPAT)
+    rng = np.random.default_rng(vocab)
+    lens = [96, 33]
+    toks = rng.integers(0, vocab, sum(lens)).astype(np.uint32)
+    inp, tgt = _chunk_inputs(toks, lens, 96)
+    _say(f"cumfreqs V={vocab}")
+    cum = gm.cumfreqs(inp, lens)
+    for b, n in enumerate(lens):
+        _, ref = om.trace(inp[b, :n])
+        assert np.array_equal(cum[b, :n], ref)
+    assert gm.compress_chunks(toks, 96) == om.compress_many(toks, 96, threads=4)
+
+
 def test_error_codes(gpu_shipped, amd):
     with pytest.raises(amd.CzipError) as e:
         gpu_shipped.compress_plan(np.zeros(10, np.uint32), 2048)   # past the 1024-entry RoPE LUT
