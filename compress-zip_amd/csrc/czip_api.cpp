@@ -74,6 +74,14 @@ struct czip_job {
     int32_t* x = nullptr;
     int8_t *xn = nullptr, *q8 = nullptr, *kc = nullptr, *vc = nullptr, *attn = nullptr, *y8 = nullptr, *r8 = nullptr;
     int32_t* logits = nullptr;
+    // decompress
+    int S = 0;  // streams decoded together
+    int64_t total_tokens = 0;
+    std::vector<int32_t> h_ntok;
+    uint8_t* d_data = nullptr;
+    int64_t *d_offs = nullptr, *d_toff = nullptr, *st_bpos = nullptr;
+    int32_t *d_blen = nullptr, *d_ntok = nullptr, *st_bit = nullptr;
+    uint32_t *d_tokens = nullptr, *st_low = nullptr, *st_high = nullptr, *st_code = nullptr;
 };
 
 namespace {
@@ -359,7 +367,7 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T) {
         GemmArgs g{};
         g.A = j->xn; g.W = L.qkv_w; g.M = M; g.N = L.qkv_n; g.K = d;
         g.out8 = j->q8; g.ldo = d; g.mult = L.qkv_mult; g.shift = L.qkv_shift;
-        g.d = d; g.T = T; g.TP = pad64(T); g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads; g.KH = c->KH;
+        g.d = d; g.T = T; g.TP = pad64(T); g.pos = -1; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads; g.KH = c->KH;
         g.kc = j->kc; g.vc = j->vc; g.rcos = c->rcos; g.rsin = c->rsin;
         { Timed t(c, "gemm_qkv"); launch_gemm(g, EPI_QKV, s); }
         AttnArgs a{};
@@ -574,10 +582,13 @@ static czip_status run_compress(czip_job* j) {
     return CZIP_OK;
 }
 
+static czip_status run_decompress(czip_job* j);
+
 extern "C" czip_status czip_job_run(czip_job* j) {
     if (!j) return CZIP_E_ARG;
     HIPCHECK(j->ctx, hipSetDevice(j->ctx->device));
     if (j->kind == 0) return run_compress(j);
+    if (j->kind == 1) return run_decompress(j);
     return fail(j->ctx, CZIP_E_ARG, "unknown job kind");
 }
 
@@ -597,13 +608,155 @@ extern "C" czip_status czip_compress_fetch(czip_job* j, uint8_t* out, int64_t sl
     return CZIP_OK;
 }
 
-extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t*, const int64_t*, const int32_t*, const int32_t*,
-                                            int32_t, czip_job** out) {
-    if (out) *out = nullptr;
-    return c ? fail(c, CZIP_E_ARG, "decompress is not built yet") : CZIP_E_ARG;
+// ===========================================================================
+// Decompress job: streams of S chunks decode in lockstep, one token per
+// stream per step, through the same layer kernels as the prefill (M = S rows)
+// plus the decode attention and the fused CDF + arithmetic-decode kernel.
+// ===========================================================================
+extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t* data, const int64_t* offs, const int32_t* lens,
+                                            const int32_t* ntoks, int32_t nchunks, czip_job** out) {
+    if (!c || !out || nchunks < 0 || (nchunks > 0 && (!offs || !lens || !ntoks)))
+        return c ? fail(c, CZIP_E_ARG, "bad argument") : CZIP_E_ARG;
+    *out = nullptr;
+    if ((uint32_t)c->cfg.vocab <= BOS) return fail(c, CZIP_E_TOKEN, "BOS token 1022 is outside the vocabulary");
+    const int cap = std::min(c->cfg.context_length, c->cfg.max_seq_len);
+    int64_t total_bytes = 0, total_tokens = 0;
+    int Tcap = 1;
+    for (int i = 0; i < nchunks; i++) {
+        if (lens[i] < 0 || offs[i] < 0 || ntoks[i] < 0) return fail(c, CZIP_E_ARG, "negative chunk length/offset");
+        if (ntoks[i] > cap) return fail(c, CZIP_E_RANGE, "chunk token count exceeds the RoPE LUT / KV cache");
+        total_bytes = std::max<int64_t>(total_bytes, offs[i] + lens[i]);
+        total_tokens += ntoks[i];
+        Tcap = std::max(Tcap, (int)ntoks[i]);
+    }
+    if (total_bytes > 0 && !data) return fail(c, CZIP_E_ARG, "null data");
+    HIPCHECK(c, hipSetDevice(c->device));
+    auto j = std::make_unique<czip_job>();
+    j->ctx = c;
+    j->kind = 1;
+    j->nchunks = nchunks;
+    j->T = Tcap;
+    j->total_tokens = total_tokens;
+    j->h_ntok.assign(ntoks, ntoks + nchunks);
+    const size_t d = (size_t)c->cfg.d_model, L = (size_t)c->cfg.n_layers;
+    double gb = 16.0;
+    if (const char* s = getenv("CZIP_SCRATCH_GB")) gb = atof(s);
+    const double per_stream = (double)row_bytes(c) + 2.0 * L * (double)c->KH * Tcap * 64 + 64;
+    int64_t S = (int64_t)(gb * 1e9 / per_stream);
+    if (const char* s = getenv("CZIP_DECODE_STREAMS")) S = std::min<int64_t>(S, atoll(s));
+    S = std::max<int64_t>(1, std::min<int64_t>(S, std::max(nchunks, 1)));
+    j->S = (int)S;
+    std::vector<int64_t> toff((size_t)std::max(nchunks, 1), 0);
+    for (int i = 1; i < nchunks; i++) toff[(size_t)i] = toff[(size_t)i - 1] + ntoks[i - 1];
+    czip_status rc = CZIP_OK;
+    auto& A = j->allocs;
+    const size_t nc = (size_t)std::max(nchunks, 1);
+    if ((rc = dalloc(c, A, &j->d_data, (size_t)std::max<int64_t>(total_bytes, 1))) ||
+        (rc = dalloc(c, A, &j->d_offs, nc)) || (rc = dalloc(c, A, &j->d_blen, nc)) ||
+        (rc = dalloc(c, A, &j->d_ntok, nc)) || (rc = dalloc(c, A, &j->d_toff, nc)) ||
+        (rc = dalloc(c, A, &j->d_tokens, (size_t)std::max<int64_t>(total_tokens, 1))) ||
+        (rc = dalloc(c, A, &j->st_low, (size_t)S)) || (rc = dalloc(c, A, &j->st_high, (size_t)S)) ||
+        (rc = dalloc(c, A, &j->st_code, (size_t)S)) || (rc = dalloc(c, A, &j->st_bpos, (size_t)S)) ||
+        (rc = dalloc(c, A, &j->st_bit, (size_t)S)) || (rc = dalloc(c, A, &j->inp, (size_t)S)) ||
+        (rc = dalloc(c, A, &j->x, (size_t)S * d)) || (rc = dalloc(c, A, &j->xn, (size_t)S * d)) ||
+        (rc = dalloc(c, A, &j->q8, (size_t)S * d)) || (rc = dalloc(c, A, &j->attn, (size_t)S * d)) ||
+        (rc = dalloc(c, A, &j->y8, (size_t)S * d)) || (rc = dalloc(c, A, &j->r8, (size_t)S * c->cfg.d_ff)) ||
+        (rc = dalloc(c, A, &j->logits, (size_t)S * c->cfg.vocab)) ||
+        (rc = dalloc(c, A, &j->kc, L * (size_t)S * c->KH * Tcap * 64)) ||
+        (rc = dalloc(c, A, &j->vc, L * (size_t)S * c->KH * Tcap * 64))) {
+        free_job_mem(j.get());
+        return rc;
+    }
+    hipError_t e = hipSuccess;
+    if (total_bytes > 0) e = hipMemcpy(j->d_data, data, (size_t)total_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess && nchunks > 0) e = hipMemcpy(j->d_offs, offs, (size_t)nchunks * 8, hipMemcpyHostToDevice);
+    if (e == hipSuccess && nchunks > 0) e = hipMemcpy(j->d_blen, lens, (size_t)nchunks * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess && nchunks > 0) e = hipMemcpy(j->d_ntok, ntoks, (size_t)nchunks * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess && nchunks > 0) e = hipMemcpy(j->d_toff, toff.data(), (size_t)nchunks * 8, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        free_job_mem(j.get());
+        return fail(c, CZIP_E_HIP, hipGetErrorString(e));
+    }
+    *out = j.release();
+    return CZIP_OK;
 }
 
-extern "C" czip_status czip_decompress_fetch(czip_job*, uint32_t*, const int64_t*) { return CZIP_E_ARG; }
+static czip_status run_decompress(czip_job* j) {
+    czip_ctx* c = j->ctx;
+    hipStream_t s = c->stream;
+    const int d = c->cfg.d_model, F = c->cfg.d_ff, V = c->cfg.vocab, H = c->cfg.n_heads;
+    const int Tc = j->T;
+    const size_t layer_kv = (size_t)j->S * c->KH * Tc * 64;
+    for (int64_t g0 = 0; g0 < j->nchunks; g0 += j->S) {
+        const int S = (int)std::min<int64_t>(j->S, j->nchunks - g0);
+        int steps = 0;
+        for (int i = 0; i < S; i++) steps = std::max(steps, j->h_ntok[(size_t)(g0 + i)]);
+        DecState st{j->st_low, j->st_high, j->st_code, j->st_bpos, j->st_bit};
+        DecStreams ds{j->d_data, j->d_offs + g0, j->d_blen + g0, j->d_ntok + g0, j->d_tokens, j->d_toff + g0};
+        { Timed t(c, "dec_init"); launch_dec_init(st, ds, S, s); }
+        for (int p = 0; p < steps; p++) {
+            { Timed t(c, "dec_prep"); launch_dec_prep(ds, S, p, j->inp, s); }
+            { Timed t(c, "embed_norm"); launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, S, d, j->x, j->xn, s); }
+            for (int l = 0; l < c->cfg.n_layers; l++) {
+                const DevLayer& L = c->layers[(size_t)l];
+                int8_t* kc = j->kc + (size_t)l * layer_kv;
+                int8_t* vc = j->vc + (size_t)l * layer_kv;
+                GemmArgs g{};
+                g.A = j->xn; g.W = L.qkv_w; g.M = S; g.N = L.qkv_n; g.K = d;
+                g.out8 = j->q8; g.ldo = d; g.mult = L.qkv_mult; g.shift = L.qkv_shift;
+                g.d = d; g.T = Tc; g.TP = Tc; g.pos = p; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
+                g.KH = c->KH; g.kc = kc; g.vc = vc; g.rcos = c->rcos; g.rsin = c->rsin;
+                { Timed t(c, "gemm_qkv"); launch_gemm(g, EPI_QKV, s); }
+                AttnArgs a{};
+                a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = Tc; a.lens = j->d_ntok + g0; a.score_mult = L.score_mult;
+                a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = S; a.T = Tc; a.H = H; a.G = c->cfg.n_kv_heads;
+                a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;
+                { Timed t(c, "attn_decode"); launch_attn_decode(a, S, p, s); }
+                GemmArgs o{};
+                o.A = j->attn; o.W = L.out_w; o.M = S; o.N = d; o.K = d; o.out8 = j->y8; o.ldo = d;
+                o.mult = L.out_mult; o.shift = L.out_shift;
+                { Timed t(c, "gemm_o"); launch_gemm(o, EPI_REQ, s); }
+                { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.ffn_norm, L.post_attn_norm, S, d, j->xn, s); }
+                GemmArgs u{};
+                u.A = j->xn; u.W = L.up_w; u.M = S; u.N = 2 * F; u.K = d; u.out8 = j->r8; u.ldo = F;
+                u.mult = L.up_mult; u.shift = L.up_shift;
+                { Timed t(c, "gemm_up"); launch_gemm(u, EPI_REGLU, s); }
+                GemmArgs dn{};
+                dn.A = j->r8; dn.W = L.down_w; dn.M = S; dn.N = d; dn.K = F; dn.out8 = j->y8; dn.ldo = d;
+                dn.mult = L.down_mult; dn.shift = L.down_shift;
+                { Timed t(c, "gemm_down"); launch_gemm(dn, EPI_REQ, s); }
+                const int8_t* next = (l + 1 < c->cfg.n_layers) ? c->layers[(size_t)l + 1].attn_norm : c->final_norm;
+                { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.post_ffn_norm, next, S, d, j->xn, s); }
+            }
+            GemmArgs hd{};
+            hd.A = j->xn; hd.W = c->head_w; hd.M = S; hd.N = V; hd.K = d; hd.out32 = j->logits; hd.ldo = V;
+            { Timed t(c, "gemm_head"); launch_gemm(hd, EPI_RAW, s); }
+            { Timed t(c, "cdf_decode"); launch_cdf_decode(j->logits, S, V, c->lut, c->cfg.coef_q24, c->cfg.target_total, p, st, ds, s); }
+        }
+    }
+    HIPCHECK(c, hipGetLastError());
+    HIPCHECK(c, hipStreamSynchronize(s));
+    resolve_events(c);
+    return CZIP_OK;
+}
+
+extern "C" czip_status czip_decompress_fetch(czip_job* j, uint32_t* tokens_out, const int64_t* tok_offs) {
+    if (!j || j->kind != 1 || (j->total_tokens > 0 && !tokens_out)) return CZIP_E_ARG;
+    czip_ctx* c = j->ctx;
+    if (j->total_tokens == 0) return CZIP_OK;
+    if (!tok_offs) {
+        HIPCHECK(c, hipMemcpy(tokens_out, j->d_tokens, (size_t)j->total_tokens * 4, hipMemcpyDeviceToHost));
+        return CZIP_OK;
+    }
+    std::vector<uint32_t> all((size_t)j->total_tokens);
+    HIPCHECK(c, hipMemcpy(all.data(), j->d_tokens, all.size() * 4, hipMemcpyDeviceToHost));
+    int64_t src = 0;
+    for (int64_t i = 0; i < j->nchunks; i++) {
+        memcpy(tokens_out + tok_offs[i], all.data() + src, (size_t)j->h_ntok[(size_t)i] * 4);
+        src += j->h_ntok[(size_t)i];
+    }
+    return CZIP_OK;
+}
 
 extern "C" void czip_job_free(czip_job* j) {
     if (!j) return;

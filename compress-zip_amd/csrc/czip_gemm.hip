@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                     a.out8[(size_t)row * a.ldo + (col_base >> 1) + j * 16 + lc] = (int8_t)clamp127(sra_rne32(gr * u, 7));
                 }
             } else {  // EPI_QKV
-                const int p = row % a.T, b = row / a.T;
+                const int p = a.pos >= 0 ? a.pos : row % a.T, b = a.pos >= 0 ? row : row / a.T;
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
                     const int i32 = j * 16 + lc;  // rotary pair (i32, i32 + 32)
@@ -108,8 +108,13 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
                             size_t off = (((size_t)b * a.KH + g) * a.T + p) * 64;
                             a.kc[off + i32] = (int8_t)clamp127(sra_rne32(xr, 15));
                             a.kc[off + i32 + 32] = (int8_t)clamp127(sra_rne32(yr, 15));
+                        } else if (a.pos >= 0) {
+                            // V of a decode step: key-major like K
+                            size_t off = (((size_t)b * a.KH + g) * a.T + p) * 64;
+                            a.vc[off + i32] = (int8_t)xv;
+                            a.vc[off + i32 + 32] = (int8_t)yv;
                         } else {
-                            // V, stored dim-major for the PV operand
+                            // V, stored dim-major for the prefill PV operand
                             size_t off = (((size_t)b * a.KH + g) * 64) * a.TP + p;
                             a.vc[off + (size_t)i32 * a.TP] = (int8_t)xv;
                             a.vc[off + (size_t)(i32 + 32) * a.TP] = (int8_t)yv;

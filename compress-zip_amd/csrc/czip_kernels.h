@@ -26,7 +26,8 @@ struct GemmArgs {
     int d, T, kv_mode, G, KH;
     int TP;           // V^T row stride: T rounded up to a multiple of 64
     int8_t* kc;       // [B, KH, T, 64]   rotated keys
-    int8_t* vc;       // [B, KH, 64, TP]  values, transposed (dim-major)
+    int8_t* vc;       // [B, KH, 64, TP]  values, transposed (dim-major); decode: [B, KH, T, 64]
+    int pos;          // >= 0: every row is at this position and row = chunk (decode step)
     const int16_t* rcos;
     const int16_t* rsin;
 };
@@ -60,5 +61,30 @@ void launch_cdf(const int32_t* logits, int M, int V, const uint32_t* targets, co
                 hipStream_t s);
 void launch_encode(const uint32_t* lohi, const int32_t* lens, int nb, int T, unsigned total, uint8_t* out,
                    int64_t slot, int32_t* out_lens, int32_t* err, hipStream_t s);
+
+// ---- batched decode (decompression) ----
+struct DecState {        // one arithmetic decoder per stream (arith_coder.rs:139-164)
+    uint32_t* low;
+    uint32_t* high;
+    uint32_t* code;
+    int64_t* byte_pos;
+    int32_t* bit_pos;
+};
+struct DecStreams {      // per stream of the current group
+    const uint8_t* data;      // all chunk bytes
+    const int64_t* offs;      // [S] byte offset of the stream's chunk
+    const int32_t* blen;      // [S] byte length
+    const int32_t* ntok;      // [S] tokens to decode
+    uint32_t* tokens;         // all decoded tokens
+    const int64_t* tok_offs;  // [S] output offset of the stream's tokens
+};
+void launch_dec_init(DecState st, DecStreams ds, int S, hipStream_t s);
+// inputs of step p: BOS at p = 0, else the token decoded at p - 1; rows past ntok get 0
+void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s);
+// one query per (stream, head) at position p over cached keys 0..p
+void launch_attn_decode(const AttnArgs& a, int S, int p, hipStream_t s);
+// logits -> cumulative frequencies -> one arithmetic-decode step (arith_coder.rs:195-264)
+void launch_cdf_decode(const int32_t* logits, int S, int V, const uint16_t* lut, unsigned coef, unsigned total,
+                       int p, DecState st, DecStreams ds, hipStream_t s);
 
 }  // namespace czip

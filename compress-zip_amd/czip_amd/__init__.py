@@ -216,6 +216,28 @@ class Model:
         finally:
             job.free()
 
+    # --- decompression on the device ---
+    def decompress_plan(self, chunks, ntoks) -> "DecodeJob":
+        lens = np.array([len(c) for c in chunks], np.int32)
+        offs = np.zeros(len(chunks), np.int64)
+        if len(chunks) > 1:
+            offs[1:] = np.cumsum(lens[:-1])
+        data = np.frombuffer(b"".join(chunks) + b"\0", np.uint8).copy()
+        ntoks = np.ascontiguousarray(ntoks, dtype=np.int32)
+        h = C.c_void_p()
+        self._check(lib().czip_decompress_plan(self._ctx, _p(data), _p(offs), _p(lens), _p(ntoks), len(chunks),
+                                               C.byref(h)))
+        return DecodeJob(self, h, int(ntoks.sum()))
+
+    def decompress_chunks(self, chunks, ntoks) -> np.ndarray:
+        """Decoded tokens of every chunk, concatenated (main.rs:377-399)."""
+        job = self.decompress_plan(chunks, ntoks)
+        try:
+            job.run()
+            return job.fetch()
+        finally:
+            job.free()
+
     # --- instrumentation ---
     def set_profiling(self, on: bool):
         lib().czip_set_profiling(self._ctx, 1 if on else 0)
@@ -254,3 +276,14 @@ class Job:
 
     def __del__(self):
         self.free()
+
+
+class DecodeJob(Job):
+    def __init__(self, model: Model, handle, total_tokens: int):
+        super().__init__(model, handle, 0)
+        self.total_tokens = total_tokens
+
+    def fetch(self):
+        out = np.zeros(max(self.total_tokens, 1), np.uint32)
+        self.model._check(lib().czip_decompress_fetch(self.h, _p(out), None))
+        return out[:self.total_tokens]

@@ -161,6 +161,44 @@ def test_cdf_large_vocab(amd, orc, tmp_path, vocab):
     assert gm.compress_chunks(toks, 96) == om.compress_many(toks, 96, threads=4)
 
 
+@pytest.mark.parametrize("chunk", [64, 512])
+def test_decompress_shipped(gpu_shipped, shipped, chunk):
+    """Batched device decode of oracle-coded chunks recovers the tokens
+    (main.rs:377-396), ragged last chunk included."""
+    rng = np.random.default_rng(50 + chunk)
+    n = chunk * 3 + chunk // 2 + 1
+    toks = rng.integers(0, 1024, n).astype(np.uint32)
+    chunks = shipped.compress_many(toks, chunk, threads=8)
+    ntoks = [min(chunk, n - c * chunk) for c in range(len(chunks))]
+    _say(f"decompress shipped chunk={chunk} n={n}")
+    out = gpu_shipped.decompress_chunks(chunks, ntoks)
+    assert np.array_equal(out, toks)
+
+
+def test_decompress_random_models(amd, orc, random_models):
+    from czip_amd import synth
+    for name, kv, vocab, chunk in [("d512", amd.KV_RUST_COMPAT, 1024, 128), ("d768", amd.KV_GQA, 8192, 64),
+                                   ("sink", amd.KV_RUST_COMPAT, 1024, 96)]:
+        gm, om = _model_pair(amd, orc, random_models[name], kv)
+        toks = synth.zipf_ids(chunk * 2 + 17, vocab, seed=60)
+        _say(f"decompress {name} chunk={chunk}")
+        chunks = gm.compress_chunks(toks, chunk)
+        assert chunks == om.compress_many(toks, chunk, threads=8)
+        ntoks = [chunk, chunk, 17]
+        assert np.array_equal(gm.decompress_chunks(chunks, ntoks), toks)
+
+
+def test_decompress_stream_groups(gpu_shipped, shipped, monkeypatch):
+    """More chunks than streams per group: groups run one after the other."""
+    monkeypatch.setenv("CZIP_DECODE_STREAMS", "3")
+    rng = np.random.default_rng(70)
+    toks = rng.integers(0, 1024, 64 * 7 + 5).astype(np.uint32)
+    chunks = gpu_shipped.compress_chunks(toks, 64)
+    ntoks = [64] * 7 + [5]
+    out = gpu_shipped.decompress_chunks(chunks, ntoks)
+    assert np.array_equal(out, toks)
+
+
 def test_error_codes(gpu_shipped, amd):
     with pytest.raises(amd.CzipError) as e:
         gpu_shipped.compress_plan(np.zeros(10, np.uint32), 2048)   # past the 1024-entry RoPE LUT
