@@ -90,6 +90,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-decompress", action="store_true", help="skip the decompress leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--tokens", type=int, default=0, help="truncate the workload (profiling runs only)")
     args = ap.parse_args()
@@ -160,6 +161,31 @@ def main():
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "kernel": dom}
 
+    # decompress leg: the chunks just coded, decoded back on the device as
+    # concurrent streams (one token per stream per step), checked for identity
+    dec = None
+    if not args.no_decompress:
+        ntoks = [min(chunk, n - c * chunk) for c in range(len(chunks))]
+        djob = model.decompress_plan(chunks, ntoks)
+        model.reset_stats()
+        model.set_profiling(True)
+        t0 = time.perf_counter()
+        djob.run()
+        t1 = time.perf_counter()
+        model.set_profiling(False)
+        back = djob.fetch()
+        djob.free()
+        if not np.array_equal(back, tokens):
+            raise SystemExit("decompressed tokens differ from the input")
+        dk = {}
+        for name in ["dec_init", "dec_prep", "embed_norm", "gemm_qkv", "attn_decode", "gemm_o", "row_norm",
+                     "gemm_up", "gemm_down", "gemm_head", "cdf_decode"]:
+            launches, tot = model.kernel_stats(name)
+            if launches:
+                dk[name] = {"ms": round(tot, 3), "launches": launches}
+        dec = {"value": round(n / (t1 - t0), 1), "unit": "tok/s", "ms": round((t1 - t0) * 1000, 2),
+               "streams": len(chunks), "roundtrip_exact": True, "kernels": dk}
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
@@ -173,6 +199,7 @@ def main():
                    "chunks": len(chunks), "kv_mode": "rust_compat", "parallelism": "chunks"},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "decompress": dec,
         "gemm_int8_tops": round(gemm_tops, 2),
         "coded_bytes": coded,
         "kernels": {k: {"avg_ms": round(v["avg_ms"], 4), "ms_per_step": round(v["ms_per_step"], 3),
