@@ -30,18 +30,26 @@ WORKLOADS = {
     # shipped model, level 4, Zipf(1.1) token ids (no tokenizer step)
     "v001_L4_ctx512_zipf16M": dict(model="shipped", chunk=512, ids=16 << 20),
 }
-DEFAULT = "v001_L4_ctx512_zipf16M"
+DEFAULT = "v001_L4_ctx512_text64MiB"
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_tokens(wl, model_path, vocab):
+def make_tokens(wl, weights, vocab):
+    """Token ids of the workload and, for text workloads, the text and tokenizer."""
+    import czip_amd
     from czip_amd import synth
     if "ids" in wl:
-        return synth.zipf_ids(wl["ids"], vocab, seed=7)
-    raise SystemExit("text workloads need the tokenizer (not built yet)")
+        return synth.zipf_ids(wl["ids"], vocab, seed=7), None, None
+    t = time.perf_counter()
+    text = synth.synthetic_text(wl["text_bytes"], seed=1234)
+    tk = czip_amd.Tokenizer(weights)
+    t1 = time.perf_counter()
+    ids = tk.encode(text, threads=min(16, len(os.sched_getaffinity(0))))
+    log(f"text {len(text)} B generated in {t1 - t:.1f} s, tokenized in {time.perf_counter() - t1:.1f} s")
+    return ids, text, tk
 
 
 def gemm_ops_per_token(cfg, kv_mode):
@@ -107,7 +115,7 @@ def main():
     kv_mode = czip_amd.KV_RUST_COMPAT
     weights = czip_amd.ModelWeights(model_path, kv_mode)
     cfg = weights.config
-    tokens = make_tokens(wl, model_path, cfg["vocab_size"])
+    tokens, text, tokenizer = make_tokens(wl, weights, cfg["vocab_size"])
     if args.tokens:
         tokens = tokens[:args.tokens]
     chunk = wl["chunk"]
@@ -177,6 +185,8 @@ def main():
         djob.free()
         if not np.array_equal(back, tokens):
             raise SystemExit("decompressed tokens differ from the input")
+        if text is not None and tokenizer.decode_bytes(back) != text:
+            raise SystemExit("detokenized output differs from the input text")
         dk = {}
         for name in ["dec_init", "dec_prep", "embed_norm", "gemm_qkv", "attn_decode", "gemm_o", "row_norm",
                      "gemm_up", "gemm_down", "gemm_head", "cdf_decode"]:
@@ -196,6 +206,7 @@ def main():
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8", "data": "synthetic",
         "config": {"workload": args.workload, "model": "v001_eng.czm", "chunk_tokens": chunk, "tokens": n,
+                   "text_bytes": len(text) if text is not None else None,
                    "chunks": len(chunks), "kv_mode": "rust_compat", "parallelism": "chunks"},
         "roofline": roof,
         "cpu_baseline": cpu,

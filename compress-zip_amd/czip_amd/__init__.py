@@ -82,6 +82,12 @@ SIGNATURES = {
     "czip_chunk_slot_bytes": (C.c_int64, [C.c_int32]),
     "czip_decompress_plan": (C.c_int32, [_P, _P, _P, _P, _P, C.c_int32, C.POINTER(C.c_void_p)]),
     "czip_decompress_fetch": (C.c_int32, [_P, _P, _P]),
+    "czip_tokenizer_load": (C.c_int32, [C.c_char_p, C.c_size_t, C.POINTER(C.c_void_p)]),
+    "czip_tokenizer_from_model": (C.c_int32, [_P, C.POINTER(C.c_void_p)]),
+    "czip_tokenizer_free": (None, [_P]),
+    "czip_tokenize": (C.c_int32, [_P, C.c_char_p, C.c_size_t, C.c_int32, _P, C.c_size_t,
+                                  C.POINTER(C.c_size_t)]),
+    "czip_detokenize": (C.c_int32, [_P, _P, C.c_size_t, _P, C.c_size_t, C.POINTER(C.c_size_t)]),
     "czip_set_profiling": (None, [_P, C.c_int32]),
     "czip_kernel_stats": (C.c_int32, [_P, C.c_char_p, C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
     "czip_reset_stats": (None, [_P]),
@@ -144,6 +150,46 @@ class ModelWeights:
     def __del__(self):
         if getattr(self, "_h", None):
             lib().czip_model_free(self._h)
+            self._h = None
+
+
+class Tokenizer:
+    """The model's BPE tokenizer (rust/src/tiktoken.rs), host-side C++."""
+
+    def __init__(self, weights: "ModelWeights" = None, json_bytes: bytes = None):
+        self._h = C.c_void_p()
+        if json_bytes is not None:
+            rc = lib().czip_tokenizer_load(json_bytes, len(json_bytes), C.byref(self._h))
+        else:
+            rc = lib().czip_tokenizer_from_model(weights._h, C.byref(self._h))
+        if rc:
+            raise CzipError(rc, "tokenizer load")
+
+    def encode(self, text, threads: int = 1) -> np.ndarray:
+        """encode_with_special_tokens (tiktoken.rs:498-501) of UTF-8 text."""
+        data = text.encode("utf-8") if isinstance(text, str) else bytes(text)
+        out = np.zeros(max(len(data), 1), np.uint32)
+        n = C.c_size_t()
+        rc = lib().czip_tokenize(self._h, data, len(data), threads, _p(out), out.size, C.byref(n))
+        if rc:
+            raise CzipError(rc, "tokenize")
+        return out[:n.value].copy()
+
+    def decode_bytes(self, ids) -> bytes:
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        n = C.c_size_t()
+        rc = lib().czip_detokenize(self._h, _p(ids) if ids.size else None, ids.size, None, 0, C.byref(n))
+        if rc not in (0, -6):
+            raise CzipError(rc, "detokenize")
+        buf = np.zeros(max(n.value, 1), np.uint8)
+        rc = lib().czip_detokenize(self._h, _p(ids) if ids.size else None, ids.size, _p(buf), buf.size, C.byref(n))
+        if rc:
+            raise CzipError(rc, "detokenize")
+        return buf[:n.value].tobytes()
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().czip_tokenizer_free(self._h)
             self._h = None
 
 

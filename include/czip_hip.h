@@ -140,6 +140,26 @@ czip_status czip_decompress_plan(czip_ctx* ctx, const uint8_t* data, const int64
                                  czip_job** job);
 czip_status czip_decompress_fetch(czip_job* job, uint32_t* tokens_out, const int64_t* tok_offs);
 
+/* ---- tokenizer (host): the BPE of the text configurations.
+ *      czip_tokenizer_load replaces load_tiktoken_json_from_bytes
+ *      (rust/src/tiktoken.rs:536-563); czip_tokenizer_from_model decompresses
+ *      the model's embedded JSON like main.rs:88-109 (system libzstd /
+ *      libbrotlidec).  czip_tokenize = encode_with_special_tokens
+ *      (tiktoken.rs:215-269, 498-501) over UTF-8 text (CZIP_E_FORMAT if not
+ *      valid UTF-8); `threads` > 1 splits the text at points where no pattern
+ *      match can straddle, with identical output.  A text of `len` bytes never
+ *      yields more than `len` tokens.  czip_detokenize = decode_bytes
+ *      (tiktoken.rs:186-198).  *n_out receives the required count; a too small
+ *      `cap` gives CZIP_E_OVERFLOW. ---- */
+typedef struct czip_tokenizer czip_tokenizer;
+czip_status czip_tokenizer_load(const char* json, size_t len, czip_tokenizer** out);
+czip_status czip_tokenizer_from_model(const czip_model* m, czip_tokenizer** out);
+void        czip_tokenizer_free(czip_tokenizer* t);
+czip_status czip_tokenize(const czip_tokenizer* t, const char* text, size_t len, int32_t threads,
+                          uint32_t* out, size_t cap, size_t* n_out);
+czip_status czip_detokenize(const czip_tokenizer* t, const uint32_t* ids, size_t n, uint8_t* out,
+                            size_t cap, size_t* n_out);
+
 /* ---- instrumentation: per-kernel HIP-event timing on the context stream. ---- */
 void        czip_set_profiling(czip_ctx* ctx, int32_t on);
 /* Kernel names: "embed_norm","gemm_qkv","attention","gemm_o","row_norm",
