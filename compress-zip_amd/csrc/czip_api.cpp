@@ -26,7 +26,21 @@ struct DevLayer {
     int32_t* score_mult = nullptr;
     int qkv_mult, out_mult, up_mult, down_mult, qkv_shift, out_shift, up_shift, down_shift;
     int qkv_n;  // QKV rows the attention reads
+    int attn_general;  // attention must take its general path (see attention_needs_general)
 };
+
+// The prefill attention kernel's fast path assumes |score| < 2^30, so that
+// score differences never wrap in i32, and exp2_lut[0] == 65535, so that a
+// zero difference reads the table's first entry.  |score| <= 8 * |mult| + 1
+// (|dot| <= 64 * 127 * 127, divided by 4 and by 2^15).
+int attention_needs_general(const uint16_t* exp2_lut, const int32_t* score_mult, int n_heads) {
+    if (exp2_lut[0] != 65535) return 1;
+    for (int h = 0; h < n_heads; h++) {
+        const long long m = score_mult[h];
+        if (m >= (1ll << 27) || m <= -(1ll << 27)) return 1;
+    }
+    return 0;
+}
 
 struct Stat {
     int64_t launches = 0;
@@ -277,6 +291,7 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
         UP(D.down_w, L.down_w, d * F)
         UP(D.score_mult, L.score_mult, (size_t)w->n_heads)
         if (L.sink_key) { UP(D.sink, L.sink_key, 64) }
+        D.attn_general = attention_needs_general(w->exp2_lut, L.score_mult, w->n_heads);
         D.qkv_mult = L.qkv_mult; D.out_mult = L.out_mult; D.up_mult = L.up_mult; D.down_mult = L.down_mult;
         D.qkv_shift = L.qkv_shift; D.out_shift = L.out_shift; D.up_shift = L.up_shift; D.down_shift = L.down_shift;
     }
@@ -374,6 +389,7 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T) {
         a.q = j->q8; a.kc = j->kc; a.vc = j->vc; a.TP = pad64(T); a.lens = j->lens; a.score_mult = L.score_mult;
         a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = M; a.T = T; a.H = H; a.G = c->cfg.n_kv_heads;
         a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
+        a.general = L.attn_general;
         { Timed t(c, "attention"); launch_attention(a, nb, s); }
         GemmArgs o{};
         o.A = j->attn; o.W = L.out_w; o.M = M; o.N = d; o.K = d; o.out8 = j->y8; o.ldo = d;
@@ -711,6 +727,7 @@ static czip_status run_decompress(czip_job* j) {
                 a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = Tc; a.lens = j->d_ntok + g0; a.score_mult = L.score_mult;
                 a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = S; a.T = Tc; a.H = H; a.G = c->cfg.n_kv_heads;
                 a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;
+                a.general = L.attn_general;
                 { Timed t(c, "attn_decode"); launch_attn_decode(a, S, p, s); }
                 GemmArgs o{};
                 o.A = j->attn; o.W = L.out_w; o.M = S; o.N = d; o.K = d; o.out8 = j->y8; o.ldo = d;

@@ -14,34 +14,73 @@ namespace czip {
 //
 // One workgroup = one chunk, one head, 64 query rows (4 waves x 16 rows).
 // Per 64-key tile each wave:
-//  1. forms S^T = K Q^T (int8 MFMA) and the score epilogue;
-//  2. scans its rows' keys in order: running max, records, weights
-//     w = E(s - max), segment ids, rescale factors (lanes own 16 keys);
-//  3. for each segment index j = 0..max records, forms the segment sums of
-//     all 16 rows at once, O_j^T = V^T P_j^T, on int8 MFMA.  The 16-bit
-//     weights enter as two signed bytes: w - 32896 = 256*hi + lo, keys outside
-//     segment j carry w = 0, and the constant 32896 * sum(v) is added back;
-//  4. hands O_j through LDS to a "lanes = head dims" layout and walks each
-//     row's own segments: rescale at the record, then add (no lane waste on
-//     rows that have fewer records).
-// S^T puts query row (lane % 16) in the lane with keys 16*blk + 4*(lane/16) + r
-// in its registers, which is the B-operand layout of P^T for the PV product.
+//  1. forms S^T = K Q^T (int8 MFMA) and the score epilogue in f64, which is
+//     exact: |dot / 4 * mult| < 2^49;
+//  2. scans its rows' keys in order (a lane owns 16 consecutive keys of one
+//     row): running max, records, one exp per key.  A key's weight and, at a
+//     record, the rescale factor are both E(-|s - max before the key|);
+//  3. packs the (row, segment) pairs of its 16 rows densely into MFMA
+//     columns (a tile has ~2 records per row but up to 64), and for each
+//     group of 16 columns forms the segment sums O^T = V^T P^T on int8 MFMA.
+//     The 16-bit weights enter as two signed bytes: w - 32896 = 256*hi + lo,
+//     keys outside a column's segment carry w = 0, and 32896 * sum(v) is
+//     added back;
+//  4. walks each row's columns in order: rescale at the record, then add,
+//     with lanes = head dims for vacc and S in scalar registers.
+// Scores are kept as s ^ 2^31 so that unsigned order is signed order; 0 is
+// INT32_MIN, the reference's "nothing seen yet".
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int score_of(int dot, int mult) {
-    int du = sra_rne32(dot, 2);        // Q_SHIFT
-    return mul_sra_rne(du, mult, 15);  // sra_rne64((i64)du * mult, 15), attention.rs:233-239
-}
 
-constexpr int KLD = 80;           // LDS row stride (bytes) of the K tile and of the V^T tile
-constexpr unsigned WOFF = 32896;  // w - WOFF spans [-32896, 32639] = 256*[-128,127] + [-128,127]
+constexpr int KLD = 80;               // LDS row stride (bytes) of the K tile and of the V^T tile
+constexpr unsigned WOFF = 32896;      // w - WOFF spans [-32896, 32639] = 256*[-128,127] + [-128,127]
+constexpr unsigned BIAS = 0x80000000u;
+constexpr int RS = 68;                // row stride (words) of the per-wave buffer: 16-byte accesses of 16 rows hit 64 banks
+constexpr int MAXCOL = 16 * 65;       // (row, segment) columns of a wave-tile: 16 rows x (64 records + 1)
+
+struct AttnWaveLds {
+    unsigned buf[16][RS];    // scores [row][key]; then per pass: column sums [column][dim]
+    uint16_t rec_e[16][64];  // rescale factor at record j+1 of row r (0: nothing to rescale)
+    uint16_t col[MAXCOL];    // column -> row | segment << 4
+};
 
 __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
-// vacc / S rescale at a record (attention.rs:246-261)
+// sra_rne64(sra_rne32(dot, 2) * mult, 15) (attention.rs:233-239), biased.
+// RNE of a quotient by 2^k is symmetric, so the floor form
+// (x + 2^(k-1) - 1 + bit_k(x)) >> k equals the reference's sign-magnitude one;
+// the product is exact in f64 and rint rounds half to even.
+template <bool GEN>
+__device__ __forceinline__ unsigned score_b(int dot, double mscale) {
+    const int du = (dot + 1 + ((dot >> 2) & 1)) >> 2;
+    double r = __builtin_rint((double)du * mscale);
+    if (GEN) r = fmin(fmax(r, -2147483648.0), 2147483647.0);
+    return (unsigned)(int)r ^ BIAS;
+}
+
+// exp_q16(-neg) (lut.rs:213-235) with the table pre-shifted by 16 bits.
+// (65536 >> ip) * lut == (lut << 16) >> ip for ip <= 16, and both round to 0
+// (then clamp to 1) for ip >= 17; ip is capped at 31 like the reference's
+// early return.  neg == 0 reads lut[0], which the fast path requires to be 65535.
+__device__ __forceinline__ unsigned exp_neg(unsigned neg, const unsigned* lut32) {
+    const unsigned long long pr = (unsigned long long)neg * ATTN_COEF_Q24 + (1ull << 23);
+    const unsigned t = (unsigned)(pr >> 24);
+    const unsigned ip = min(t >> 8, 31u);
+    const unsigned x = ((lut32[t & 255u] >> ip) + 0x8000u) >> 16;
+    return max(x, 1u);
+}
+
+// vacc rescale at a record (attention.rs:246-261): ((i64)v * e +- 2^15) >> 16,
+// formed from 16-bit halves of v with 24-bit multiplies (e in 1..65535).
 __device__ __forceinline__ unsigned rescale_v(unsigned v, unsigned e) {
-    long long pr = (long long)(int)v * (long long)e;
-    pr += pr >= 0 ? (1ll << 15) : -(1ll << 15);
-    return (unsigned)(int)(pr >> 16);
+    const int vh = (int)v >> 16;
+    const unsigned t = __umul24(v & 0xFFFFu, e);
+    return (unsigned)__mul24(vh, (int)e) + (t >> 16) + ((t >> 15) & 1u) + (unsigned)((int)v >> 31);
+}
+
+// S rescale at a record (attention.rs:246-250): (S * e + 0x8000) >> 16, with
+// S < 2^32 and e < 2^16
+__device__ __forceinline__ unsigned rescale_s(unsigned S, unsigned e) {
+    return (unsigned)(((unsigned long long)S * e + 0x8000ull) >> 16);
 }
 
 // bytes of x equal to zero -> 0xFF, others -> 0x00 (exact per byte)
@@ -51,17 +90,11 @@ __device__ __forceinline__ unsigned zero_bytes_mask(unsigned x) {
     return (t >> 7) * 0xFFu;
 }
 
-// Rows are padded to 68 words so that the 16 rows of a 16-byte access cover
-// all 64 LDS banks exactly once.
-constexpr int RS = 68;
-struct AttnWaveLds {
-    unsigned buf[16][RS];    // scores, then (w | seg << 16), then one segment's V sums
-    uint16_t rec_e[16][66];  // rescale factor at record j+1 of row r (0: none)
-    int nrec[16];
-};
+__device__ __forceinline__ unsigned pick(unsigned msk, unsigned a, unsigned b) { return (a & msk) | (b & ~msk); }
 
-__global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
-    __shared__ uint16_t lut[256];
+template <bool GEN>
+__global__ __launch_bounds__(256, 3) void k_attention(AttnArgs a) {
+    __shared__ unsigned lut32[256];
     __shared__ __attribute__((aligned(16))) int8_t Ks[64 * KLD];
     __shared__ __attribute__((aligned(16))) int8_t Vt[64 * KLD];
     __shared__ __attribute__((aligned(16))) AttnWaveLds wl[4];
@@ -71,13 +104,13 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     const int q0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
     const int T = a.T, len = a.lens[b];
     if (q0 >= len) return;
-    lut[tid] = a.lut[tid];
+    lut32[tid] = (unsigned)a.lut[tid] << 16;
     AttnWaveLds& W = wl[wave];
     const int D = a.H * 64;
     const int g = a.kv_mode == 1 ? (h * a.G) / a.H : 0;
     const int8_t* Kg = a.kc + ((size_t)b * a.KH + g) * T * 64;
     const int8_t* Vg = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP;
-    const int mult = a.score_mult[h];
+    const double mscale = (double)a.score_mult[h] * (1.0 / 32768.0);
     const int p = q0 + wave * 16 + row;  // query position of this lane's row (scan / MFMA layouts)
     const int wrow0 = q0 + wave * 16;
     const bool wave_live = wrow0 < len;
@@ -86,22 +119,25 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     v4i qop = (v4i){0, 0, 0, 0};
     if (p < T) qop = *(const v4i*)(a.q + ((size_t)b * T + p) * D + h * 64 + grp * 16);
 
-    // state: running max m and weight sum S in the MFMA layout (row = lane % 16,
-    // replicated over the 4 lane groups); vacc in the "lanes = dims" layout
-    // (lane = head dim, register index = row)
-    int m = INT32_MIN;
-    unsigned long long S = 0;
+    // state: running max m (biased) with lanes = rows (replicated over the 4
+    // lane groups); vacc with lanes = head dims (register index = row); the
+    // weight sums S of the 16 rows are wave-uniform (scalar registers).  S fits
+    // in 32 bits: S <= 65535 * (T + 1) < 2^32 for T <= 65535.
+    unsigned m = 0u;
+    unsigned Sr[16];
     unsigned vacc[16];
     for (int r = 0; r < 16; r++) vacc[r] = 0;
+    unsigned s_init = 0u;
     if (a.sink) {  // attention.rs:211-224: sink score is the initial max, weight E(0) = 65535
         const int* sk = (const int*)(a.sink + grp * 16);
         int dot = 0;
         for (int i = 0; i < 4; i++) dot = __builtin_amdgcn_sdot4(qop[i], sk[i], dot, false);
         dot += __shfl_xor(dot, 16, 64);
         dot += __shfl_xor(dot, 32, 64);
-        m = score_of(dot, mult);
-        S = 65535ull;
+        m = score_b<GEN>(dot, mscale);
+        s_init = 65535u;
     }
+    for (int r = 0; r < 16; r++) Sr[r] = s_init;
 
     const int ntiles = (min(q0 + 63, len - 1)) / 64 + 1;
     for (int kt = 0; kt < ntiles; kt++) {
@@ -122,76 +158,120 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
         for (int blk = 0; blk < 4; blk++) {
             v4i kop = *(const v4i*)(Ks + (blk * 16 + row) * KLD + grp * 16);
             v4i st = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, qop, (v4i){0, 0, 0, 0}, 0, 0, 0);
-            *(int4*)&W.buf[row][blk * 16 + grp * 4] =
-                make_int4(score_of(st[0], mult), score_of(st[1], mult), score_of(st[2], mult), score_of(st[3], mult));
+            *(uint4*)&W.buf[row][blk * 16 + grp * 4] = make_uint4(score_b<GEN>(st[0], mscale), score_b<GEN>(st[1], mscale),
+                                                                  score_b<GEN>(st[2], mscale), score_b<GEN>(st[3], mscale));
         }
         wave_lds_fence();
 
         // 2. in-order scan of keys [16*grp, 16*grp+16) of this row
-        int sv[16];
+        unsigned sv[16];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            int4 v = *(const int4*)&W.buf[row][grp * 16 + i * 4];
+            const uint4 v = *(const uint4*)&W.buf[row][grp * 16 + i * 4];
             sv[i * 4] = v.x; sv[i * 4 + 1] = v.y; sv[i * 4 + 2] = v.z; sv[i * 4 + 3] = v.w;
         }
+        const bool diag = t0 + 63 > wrow0;  // some key of the tile is after some row of the wave
         int nvalid = p - (t0 + grp * 16) + 1;  // keys t <= p are visible (causal)
         nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
-        int bmax = INT32_MIN;
+        if (diag) {
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-            if (k < nvalid) bmax = max(bmax, sv[k]);
-        const int e1 = __shfl(bmax, (lane - 16) & 63, 64), e2 = __shfl(bmax, (lane - 32) & 63, 64),
-                  e3 = __shfl(bmax, (lane - 48) & 63, 64);
-        int cur0 = m;
+            for (int k = 0; k < 16; k++)
+                if (k >= nvalid) sv[k] = 0u;  // INT32_MIN: never a record; weight masked below
+        }
+        unsigned bmax = 0u;
+#pragma unroll
+        for (int k = 0; k < 16; k++) bmax = max(bmax, sv[k]);
+        const unsigned e1 = __shfl(bmax, (lane - 16) & 63, 64), e2 = __shfl(bmax, (lane - 32) & 63, 64),
+                       e3 = __shfl(bmax, (lane - 48) & 63, 64);
+        unsigned cur0 = m;
         if (grp >= 1) cur0 = max(cur0, e1);
         if (grp >= 2) cur0 = max(cur0, e2);
         if (grp >= 3) cur0 = max(cur0, e3);
-        int cur = cur0, nrec = 0;
+        // weights and rescale factors: one exp per key, no branches, so the
+        // 16 table reads can be in flight together
+        unsigned xs[16];
+        unsigned recm = 0u;  // bit k: key k is a record
+        unsigned M = cur0;
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-            if (k < nvalid && sv[k] > cur) { nrec++; cur = sv[k]; }
+        for (int k = 0; k < 16; k++) {
+            const unsigned s = sv[k];
+            const bool rec = s > M;
+            unsigned x;
+            if (GEN) {
+                const int d = rec ? (int)(M - s) : (int)(s - M);  // i32 wrap, as the reference
+                x = d >= 0 ? 65535u : exp_neg(0u - (unsigned)d, lut32);
+            } else {
+                x = exp_neg(max(s, M) - min(s, M), lut32);
+            }
+            // a record over "nothing seen" (biased 0) has no rescale; in the fast
+            // path only the lane's first key can meet M == 0 as a record
+            if (GEN || k == 0) x = (rec && M == 0u) ? 0u : x;
+            xs[k] = x;
+            recm |= (rec ? 1u : 0u) << k;
+            M = max(M, s);
+        }
+        // records before this lane's keys in the row
+        const int nrec = __builtin_popcount(recm);
         const int r1 = __shfl(nrec, (lane - 16) & 63, 64), r2 = __shfl(nrec, (lane - 32) & 63, 64),
                   r3 = __shfl(nrec, (lane - 48) & 63, 64);
         int seg = (grp >= 1 ? r1 : 0) + (grp >= 2 ? r2 : 0) + (grp >= 3 ? r3 : 0);
-        cur = cur0;
-        // The PV operands use this lane's 16 consecutive keys (byte k = key 16*grp + k)
-        // in both A (V^T) and B (P^T), so the weights stay in registers.
-        unsigned hi_dw[4] = {0, 0, 0, 0}, lo_dw[4] = {0, 0, 0, 0}, sg_dw[4] = {0, 0, 0, 0};
+        // rescale factors of the records, segment ids and weights as signed
+        // byte pairs; byte k of a dword = key 16*grp + 4*i + k
+        unsigned hi_dw[4], lo_dw[4], sg_dw[4];
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            unsigned w = 0, sb = 0xFFu;  // invalid keys: weight 0, no segment
-            if (k < nvalid) {
-                const int s = sv[k];
-                if (s > cur) {
-                    W.rec_e[row][seg] = (uint16_t)(cur != INT32_MIN
-                                                       ? exp_q16((int)((unsigned)cur - (unsigned)s), lut, ATTN_COEF_Q24)
-                                                       : 0u);
+        for (int i = 0; i < 4; i++) {
+            unsigned w4[4];
+            unsigned sg = 0u;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const bool rec = (recm >> (i * 4 + k)) & 1u;
+                if (rec) {
+                    W.rec_e[row][seg] = (uint16_t)xs[i * 4 + k];
                     seg++;
-                    cur = s;
-                    w = 65535u;
-                } else {
-                    w = exp_q16((int)((unsigned)s - (unsigned)cur), lut, ATTN_COEF_Q24);
                 }
-                sb = (unsigned)seg;
+                w4[k] = rec ? 65535u : xs[i * 4 + k];
+                sg |= (unsigned)seg << (8 * k);
             }
-            const int wq = (int)w - (int)WOFF;  // [-32896, 32639] = 256*hi + lo
-            const int lo = ((wq + 128) & 255) - 128;
-            const int hi = (wq - lo) >> 8;
-            hi_dw[k >> 2] |= ((unsigned)hi & 255u) << (8 * (k & 3));
-            lo_dw[k >> 2] |= ((unsigned)lo & 255u) << (8 * (k & 3));
-            sg_dw[k >> 2] |= sb << (8 * (k & 3));
+            const unsigned p01 = __builtin_amdgcn_perm(w4[1], w4[0], 0x05010400u);
+            const unsigned p23 = __builtin_amdgcn_perm(w4[3], w4[2], 0x05010400u);
+            lo_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;
+            hi_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
+            sg_dw[i] = sg;
         }
-        int mrow = max(cur, __shfl_xor(cur, 16, 64));
-        mrow = max(mrow, __shfl_xor(mrow, 32, 64));
-        m = mrow;
+        if (diag) {  // keys after the row: weight 0 (bytes 0x80), no segment (0xFF)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int q = nvalid - 4 * i;
+                const unsigned vm = q >= 4 ? 0xFFFFFFFFu : (q <= 0 ? 0u : ((1u << (8 * q)) - 1u));
+                hi_dw[i] = pick(vm, hi_dw[i], 0x80808080u);
+                lo_dw[i] = pick(vm, lo_dw[i], 0x80808080u);
+                sg_dw[i] = pick(vm, sg_dw[i], 0xFFFFFFFFu);
+            }
+        }
+        {
+            unsigned mr = max(M, (unsigned)__shfl_xor((int)M, 16, 64));
+            m = max(mr, (unsigned)__shfl_xor((int)mr, 32, 64));
+        }
         int nrow = nrec + __shfl_xor(nrec, 16, 64);
         nrow += __shfl_xor(nrow, 32, 64);
-        if (grp == 0) W.nrec[row] = nrow;
-        int nmax = nrow;
-        for (int o = 1; o < 16; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
-        wave_lds_fence();
 
-        // 3. A operand of the PV product: V^T row (head dim 16*db + lane % 16), keys 16*grp .. +16
+        // 3. row r owns columns base_r .. base_r + nrow_r (segment j = column - base_r)
+        const int ncol = nrow + 1;
+        int incl = ncol;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            const int t = __shfl_up(incl, o, 16);
+            if (row >= o) incl += t;
+        }
+        const int base = incl - ncol;
+        int bs[17];
+#pragma unroll
+        for (int r = 0; r < 16; r++) bs[r] = __builtin_amdgcn_readlane(base, r);
+        const int C = __builtin_amdgcn_readlane(incl, 15);
+        bs[16] = C;
+        for (int j = grp; j < ncol; j += 4) W.col[base + j] = (uint16_t)(row | (j << 4));
+
+        // A operand of the PV product: V^T row (head dim 16*db + lane % 16), keys 16*grp .. +16
         v4i vop[4];
 #pragma unroll
         for (int db = 0; db < 4; db++) vop[db] = *(const v4i*)(Vt + (db * 16 + row) * KLD + grp * 16);
@@ -204,33 +284,34 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
             for (int i = 0; i < 16; i++) cs = __builtin_amdgcn_sdot4(vrow[i], 0x01010101, cs, false);
             corr = (unsigned)cs * WOFF;
         }
-        int nr[16];
-#pragma unroll
-        for (int r = 0; r < 16; r++) nr[r] = __builtin_amdgcn_readfirstlane(W.nrec[r]);
+        wave_lds_fence();
 
-        for (int j = 0; j <= nmax; j++) {
-            const unsigned jb = (unsigned)j * 0x01010101u;
+        for (int c0 = 0; c0 < C; c0 += 16) {
+            // B operand of column c0 + lane % 16: its row's weights, masked to its segment
+            const int gc = c0 + row;
+            const unsigned info = gc < C ? (unsigned)W.col[gc] : 0xFE0u;  // segment 0xFE matches no key
+            const unsigned jcol = info >> 4;
+            // rescale factor at the column's record (0: segment 0, or nothing to rescale)
+            const unsigned ecol = (jcol >= 1u && jcol < 0xFEu) ? (unsigned)W.rec_e[info & 15u][jcol - 1u] : 0u;
+            const int src = (int)(info & 15u) + 16 * grp;
+            const unsigned jb = jcol * 0x01010101u;
             v4i bh, bl;
-            int sh = 0;
+            int sh = 0, sl = 0;
 #pragma unroll
-            for (int blk = 0; blk < 4; blk++) {
-                const unsigned msk = zero_bytes_mask(sg_dw[blk] ^ jb);
-                bh[blk] = (int)((hi_dw[blk] & msk) | (0x80808080u & ~msk));
-                bl[blk] = (int)((lo_dw[blk] & msk) | (0x80808080u & ~msk));
-                sh = __builtin_amdgcn_sdot4(bh[blk], 0x01010101, sh, false);
+            for (int i = 0; i < 4; i++) {
+                const unsigned hd = (unsigned)__shfl((int)hi_dw[i], src, 64);
+                const unsigned ld = (unsigned)__shfl((int)lo_dw[i], src, 64);
+                const unsigned sd = (unsigned)__shfl((int)sg_dw[i], src, 64);
+                const unsigned msk = zero_bytes_mask(sd ^ jb);
+                bh[i] = (int)pick(msk, hd, 0x80808080u);
+                bl[i] = (int)pick(msk, ld, 0x80808080u);
+                sh = __builtin_amdgcn_sdot4(bh[i], 0x01010101, sh, false);
+                sl = __builtin_amdgcn_sdot4(bl[i], 0x01010101, sl, false);
             }
-            int sl = 0;
-#pragma unroll
-            for (int blk = 0; blk < 4; blk++) sl = __builtin_amdgcn_sdot4(bl[blk], 0x01010101, sl, false);
-            int sw = sh * 256 + sl;  // sum over this lane's 16 keys of (w_j - 32896)
+            int sw = sh * 256 + sl;  // sum over this lane's 16 keys of (w - 32896)
             sw += __shfl_xor(sw, 16, 64);
             sw += __shfl_xor(sw, 32, 64);
-            // S of this lane's row: rescale at record j, then add segment j
-            if (j >= 1 && j <= nrow) {
-                const unsigned e = W.rec_e[row][j - 1];
-                if (e) S = (S * e + 0x8000ull) >> 16;
-            }
-            S += (unsigned)(sw + 64 * (int)WOFF);
+            const unsigned swc = (unsigned)sw + 64u * WOFF;  // the column's weight sum
 #pragma unroll
             for (int db = 0; db < 4; db++) {
                 v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[db], bh, (v4i){0, 0, 0, 0}, 0, 0, 0);
@@ -239,31 +320,36 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
                 *(int4*)&W.buf[row][db * 16 + grp * 4] = make_int4(acc[0], acc[1], acc[2], acc[3]);
             }
             wave_lds_fence();
-            // 4. lanes = dims: apply segment j of every row that has one
+            // 4. the pass's columns, lanes = head dims: all 16 read at once, then
+            // walked row by row (the rows' columns are consecutive and in order)
+            unsigned bv[16];
+#pragma unroll
+            for (int c = 0; c < 16; c++) bv[c] = W.buf[c][lane];
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                if (j <= nr[r]) {
-                    const unsigned add = (unsigned)(int)W.buf[r][lane] + corr;
-                    if (j >= 1) {
-                        const unsigned e = W.rec_e[r][j - 1];
-                        if (e) vacc[r] = rescale_v(vacc[r], e);
+                const int lo = max(bs[r], c0), hi = min(bs[r + 1], c0 + 16);
+                for (int g2 = lo; g2 < hi; g2++) {
+                    const int c = g2 - c0;
+                    const unsigned e = (unsigned)__builtin_amdgcn_readlane((int)ecol, c);
+                    const unsigned swv = (unsigned)__builtin_amdgcn_readlane((int)swc, c);
+                    if (e) {
+                        vacc[r] = rescale_v(vacc[r], e);
+                        Sr[r] = rescale_s(Sr[r], e);
                     }
-                    vacc[r] += add;
+                    vacc[r] += bv[c] + corr;
+                    Sr[r] += swv;
                 }
             }
             wave_lds_fence();
         }
     }
     if (!wave_live) return;
-    // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r
+    // normalize (attention.rs:278-285): lane = head dim
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-        const unsigned slo = (unsigned)__shfl((int)(unsigned)S, r, 64);
-        const unsigned shi = (unsigned)__shfl((int)(unsigned)(S >> 32), r, 64);
         const int pr = wrow0 + r;
         if (pr < len) {
-            const unsigned long long Sr = ((unsigned long long)shi << 32) | slo;
-            const unsigned long long den = Sr == 0 ? 1ull : Sr;
+            const unsigned long long den = Sr[r] == 0u ? 1ull : (unsigned long long)Sr[r];
             a.out[((size_t)b * T + pr) * D + h * 64 + lane] = (int8_t)clamp127(div_rne_s32_u64((int)vacc[r], den));
         }
     }
@@ -271,7 +357,10 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
 
 void launch_attention(const AttnArgs& a, int B, hipStream_t s) {
     dim3 grid((unsigned)((a.T + 63) / 64), (unsigned)a.H, (unsigned)B);
-    hipLaunchKernelGGL(k_attention, grid, dim3(256), 0, s, a);
+    if (a.general)
+        hipLaunchKernelGGL(k_attention<true>, grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(k_attention<false>, grid, dim3(256), 0, s, a);
 }
 
 }  // namespace czip

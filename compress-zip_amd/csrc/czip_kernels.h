@@ -44,6 +44,7 @@ struct AttnArgs {
     int8_t* out;              // [M, H*64]
     int M, T, H, G, KH, kv_mode;
     unsigned coef;
+    int general;              // 1: scores may reach 2^30 or lut[0] != 65535 (wrapping score differences)
 };
 
 void launch_prep_chunks(const uint32_t* toks, int64_t n_tokens, int64_t chunk0, int nb, int T,

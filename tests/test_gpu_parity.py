@@ -142,6 +142,73 @@ def test_compress_random_d512(amd, orc, random_models):
     assert got == ref
 
 
+def _write_model(path, t, meta):
+    from czip_amd import synth
+    synth.write_czm(path, t, meta)
+    return path
+
+
+def test_attention_general_path(amd, orc, tmp_path):
+    """Scores that clamp to the i32 range and wrap in their differences, negative
+    multipliers and an exp table whose first entry is not 65535: the attention
+    kernel's general path against the oracle, with and without a sink."""
+    from czip_amd import synth
+    for sink in (False, True):
+        t, meta = synth.random_model_tensors(d=256, n_layers=1, n_heads=4, n_kv=1, d_ff=256, vocab=1024, ctx=256,
+                                             seed=50 + sink, sink=sink)
+        t["layers.0.attn.score_mult"] = np.array([1 << 30, -(1 << 30), 1 << 27, -5], np.int32)
+        lut = t["lut.exp2"].copy()
+        lut[0] = 65000
+        t["lut.exp2"] = lut
+        path = _write_model(str(tmp_path / f"gen{sink}.czm"), t, meta)
+        gm, om = _model_pair(amd, orc, path, amd.KV_RUST_COMPAT)
+        _check_logits(gm, om, 192, [192, 77], 60 + sink, 1024)
+
+
+def record_stress_weights(d, vocab):
+    """Token i embeds as 60 cos th_i on the first half of the dims and
+    127 sin th_i * s_j on the second (s_j from 0.5 to 1, so the dims round at
+    different points), th_i rising with i over [0, pi/4).  Query dims sum the
+    cos half (all positive); key dim j sums the first 64 + j dims of the sin
+    half, so the keys rise with the token id in fine steps: ~98% of the keys of
+    the test sequence are a new running max of every query's row."""
+    th = np.arange(vocab) / vocab * (np.pi / 4)
+    j = np.arange(d // 2)
+    emb = np.zeros((vocab, d), np.int8)
+    emb[:, :d // 2] = np.rint(60 * np.cos(th))[:, None].astype(np.int8)
+    emb[:, d // 2:] = np.rint(127 * np.sin(th)[:, None] * (0.5 + 0.5 * j / (d // 2 - 1))[None, :]).astype(np.int8)
+    qkv = np.zeros((d + 128, d), np.int8)
+    qkv[:d, :d // 2] = 1
+    for k in range(64):
+        qkv[d + k, d // 2:d // 2 + 64 + k] = 1
+    qkv[d + 64:, :d // 2] = ((np.arange(64) % 3) - 1)[:, None]
+    return emb, np.full(d, 64, np.int8), qkv
+
+
+def test_attention_every_key_a_record(amd, orc, tmp_path):
+    """Scores that rise with almost every key (identity RoPE, keys that grow
+    with the token id): nearly every key is a new running max for every query,
+    so a 64-key tile carries up to 64 records per row."""
+    from czip_amd import synth
+    d, vocab, T = 256, 1024, 256
+    t, meta = synth.random_model_tensors(d=d, n_layers=1, n_heads=4, n_kv=1, d_ff=256, vocab=vocab, ctx=T, seed=70)
+    t["embed.weight"], t["layers.0.attn_norm.weight"], t["layers.0.attn.qkv.weight"] = record_stress_weights(d, vocab)
+    t["layers.0.attn.qkv.shift"] = np.array(17, np.int8)
+    t["lut.rope_cos"] = np.full_like(t["lut.rope_cos"], 32767)
+    t["lut.rope_sin"] = np.zeros_like(t["lut.rope_sin"])
+    path = _write_model(str(tmp_path / "records.czm"), t, meta)
+    gm, om = _model_pair(amd, orc, path, amd.KV_RUST_COMPAT)
+    lens = [T, 131]
+    toks = np.concatenate([np.arange(0, vocab, vocab // T)[:T], np.arange(0, 131) * 7]).astype(np.uint32)
+    inp, _ = _chunk_inputs(toks, lens, T)
+    _say("forward_logits every-key-a-record")
+    got = gm.forward_logits(inp, lens)
+    for b, n in enumerate(lens):
+        ref, _ = om.trace(inp[b, :n])
+        bad = np.argwhere(got[b, :n] != ref)
+        assert bad.size == 0, f"chunk {b}: first mismatch at (pos, vocab) {bad[0].tolist()}"
+
+
 @pytest.mark.parametrize("vocab", [2048, 8192])
 def test_cdf_large_vocab(amd, orc, tmp_path, vocab):
     """The multi-wave CDF variants (V > 1024) against the oracle's tables and coded bytes."""
