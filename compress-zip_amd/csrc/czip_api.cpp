@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <cmath>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -28,6 +29,17 @@ struct DevLayer {
     int qkv_n;  // QKV rows the attention reads
     int attn_general;  // attention must take its general path (see attention_needs_general)
 };
+
+// Requantization parameters of a GEMM launch (model.rs:280-300).  The fast
+// path multiplies in f64, exact while |acc * mult| < 2^53: |acc| <= K * 127 * 128
+// < 2^27 for K <= 8192, so |mult| < 2^26 suffices.
+void set_requant(GemmArgs& g, int mult, int shift) {
+    g.mult = mult;
+    g.shift = shift;
+    const long long am = mult < 0 ? -(long long)mult : (long long)mult;
+    g.rq_fast = (am < (1ll << 26) && shift <= 62 && g.K <= 8192) ? 1 : 0;
+    g.rq_scale = shift <= 0 ? (double)mult : ldexp((double)mult, -shift);
+}
 
 // The prefill attention kernel's fast path assumes |score| < 2^30, so that
 // score differences never wrap in i32, and exp2_lut[0] == 65535, so that a
@@ -381,7 +393,7 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T) {
         const DevLayer& L = c->layers[(size_t)l];
         GemmArgs g{};
         g.A = j->xn; g.W = L.qkv_w; g.M = M; g.N = L.qkv_n; g.K = d;
-        g.out8 = j->q8; g.ldo = d; g.mult = L.qkv_mult; g.shift = L.qkv_shift;
+        g.out8 = j->q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
         g.d = d; g.T = T; g.TP = pad64(T); g.pos = -1; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads; g.KH = c->KH;
         g.kc = j->kc; g.vc = j->vc; g.rcos = c->rcos; g.rsin = c->rsin;
         { Timed t(c, "gemm_qkv"); launch_gemm(g, EPI_QKV, s); }
@@ -393,16 +405,16 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T) {
         { Timed t(c, "attention"); launch_attention(a, nb, s); }
         GemmArgs o{};
         o.A = j->attn; o.W = L.out_w; o.M = M; o.N = d; o.K = d; o.out8 = j->y8; o.ldo = d;
-        o.mult = L.out_mult; o.shift = L.out_shift;
+        set_requant(o, L.out_mult, L.out_shift);
         { Timed t(c, "gemm_o"); launch_gemm(o, EPI_REQ, s); }
         { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.ffn_norm, L.post_attn_norm, M, d, j->xn, s); }
         GemmArgs u{};
         u.A = j->xn; u.W = L.up_w; u.M = M; u.N = 2 * F; u.K = d; u.out8 = j->r8; u.ldo = F;
-        u.mult = L.up_mult; u.shift = L.up_shift;
+        set_requant(u, L.up_mult, L.up_shift);
         { Timed t(c, "gemm_up"); launch_gemm(u, EPI_REGLU, s); }
         GemmArgs dn{};
         dn.A = j->r8; dn.W = L.down_w; dn.M = M; dn.N = d; dn.K = F; dn.out8 = j->y8; dn.ldo = d;
-        dn.mult = L.down_mult; dn.shift = L.down_shift;
+        set_requant(dn, L.down_mult, L.down_shift);
         { Timed t(c, "gemm_down"); launch_gemm(dn, EPI_REQ, s); }
         const int8_t* next = (l + 1 < c->cfg.n_layers) ? c->layers[(size_t)l + 1].attn_norm : c->final_norm;
         { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.post_ffn_norm, next, M, d, j->xn, s); }
@@ -719,7 +731,7 @@ static czip_status run_decompress(czip_job* j) {
                 int8_t* vc = j->vc + (size_t)l * layer_kv;
                 GemmArgs g{};
                 g.A = j->xn; g.W = L.qkv_w; g.M = S; g.N = L.qkv_n; g.K = d;
-                g.out8 = j->q8; g.ldo = d; g.mult = L.qkv_mult; g.shift = L.qkv_shift;
+                g.out8 = j->q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
                 g.d = d; g.T = Tc; g.TP = Tc; g.pos = p; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
                 g.KH = c->KH; g.kc = kc; g.vc = vc; g.rcos = c->rcos; g.rsin = c->rsin;
                 { Timed t(c, "gemm_qkv"); launch_gemm(g, EPI_QKV, s); }
@@ -731,16 +743,16 @@ static czip_status run_decompress(czip_job* j) {
                 { Timed t(c, "attn_decode"); launch_attn_decode(a, S, p, s); }
                 GemmArgs o{};
                 o.A = j->attn; o.W = L.out_w; o.M = S; o.N = d; o.K = d; o.out8 = j->y8; o.ldo = d;
-                o.mult = L.out_mult; o.shift = L.out_shift;
+                set_requant(o, L.out_mult, L.out_shift);
                 { Timed t(c, "gemm_o"); launch_gemm(o, EPI_REQ, s); }
                 { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.ffn_norm, L.post_attn_norm, S, d, j->xn, s); }
                 GemmArgs u{};
                 u.A = j->xn; u.W = L.up_w; u.M = S; u.N = 2 * F; u.K = d; u.out8 = j->r8; u.ldo = F;
-                u.mult = L.up_mult; u.shift = L.up_shift;
+                set_requant(u, L.up_mult, L.up_shift);
                 { Timed t(c, "gemm_up"); launch_gemm(u, EPI_REGLU, s); }
                 GemmArgs dn{};
                 dn.A = j->r8; dn.W = L.down_w; dn.M = S; dn.N = d; dn.K = F; dn.out8 = j->y8; dn.ldo = d;
-                dn.mult = L.down_mult; dn.shift = L.down_shift;
+                set_requant(dn, L.down_mult, L.down_shift);
                 { Timed t(c, "gemm_down"); launch_gemm(dn, EPI_REQ, s); }
                 const int8_t* next = (l + 1 < c->cfg.n_layers) ? c->layers[(size_t)l + 1].attn_norm : c->final_norm;
                 { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.post_ffn_norm, next, S, d, j->xn, s); }

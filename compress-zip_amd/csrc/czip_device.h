@@ -30,6 +30,11 @@ __device__ __forceinline__ int sra_rne32(int v, unsigned sh) {
     return (int)((q ^ sign) - sign);
 }
 
+// sra_rne32 for 1 <= sh <= 30 and |v| < 2^31 - 2^sh: round half to even is
+// symmetric, so the floor form (v + 2^(sh-1) - 1 + bit_sh(v)) >> sh equals the
+// sign-magnitude one.
+__device__ __forceinline__ int rne_shr(int v, int sh) { return (v + (1 << (sh - 1)) - 1 + ((v >> sh) & 1)) >> sh; }
+
 // primitives.rs:49-73
 __device__ __forceinline__ int sra_rne64(long long v, unsigned sh) {
     if (sh == 0) return (int)(v < INT32_MIN ? INT32_MIN : (v > INT32_MAX ? INT32_MAX : v));

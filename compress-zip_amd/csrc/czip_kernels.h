@@ -22,6 +22,8 @@ struct GemmArgs {
     int8_t* out8;     // EPI_REQ / EPI_REGLU / Q of EPI_QKV  [M, ldo]
     int ldo;
     int mult, shift;
+    double rq_scale;  // mult * 2^-shift (mult when shift <= 0), used when rq_fast
+    int rq_fast;      // 1: |acc * mult| < 2^53, requant by one f64 multiply and rint
     // EPI_QKV
     int d, T, kv_mode, G, KH;
     int TP;           // V^T row stride: T rounded up to a multiple of 64

@@ -165,6 +165,23 @@ def test_attention_general_path(amd, orc, tmp_path):
         _check_logits(gm, om, 192, [192, 77], 60 + sink, 1024)
 
 
+def test_requant_general_path(amd, orc, tmp_path):
+    """Requantization outside the GEMMs' f64 fast path (|mult| >= 2^26, negative
+    multipliers, shift <= 0) against the oracle."""
+    from czip_amd import synth
+    t, meta = synth.random_model_tensors(d=256, n_layers=2, n_heads=4, n_kv=1, d_ff=256, vocab=1024, ctx=128, seed=80)
+    t["layers.0.attn.qkv.mult"] = np.array(1 << 27, np.int32)
+    t["layers.0.attn.qkv.shift"] = np.array(40, np.int8)
+    t["layers.0.attn.out.mult"] = np.array(-(1 << 28), np.int32)
+    t["layers.0.attn.out.shift"] = np.array(45, np.int8)
+    t["layers.0.ffn.up.mult"] = np.array(3, np.int32)
+    t["layers.0.ffn.up.shift"] = np.array(0, np.int8)
+    t["layers.1.ffn.down.mult"] = np.array(-819, np.int32)
+    path = _write_model(str(tmp_path / "rq.czm"), t, meta)
+    gm, om = _model_pair(amd, orc, path, amd.KV_RUST_COMPAT)
+    _check_logits(gm, om, 128, [128, 45], 81, 1024)
+
+
 def record_stress_weights(d, vocab):
     """Token i embeds as 60 cos th_i on the first half of the dims and
     127 sin th_i * s_j on the second (s_j from 0.5 to 1, so the dims round at
