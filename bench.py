@@ -55,7 +55,8 @@ def make_tokens(wl, weights, vocab):
 def gemm_ops_per_token(cfg, kv_mode):
     d, F, V, G = cfg["d_model"], cfg["d_ff"], cfg["vocab_size"], cfg["n_kv_heads"]
     qkv_n = d + 2 * G * 64 if kv_mode == 1 else d + 128
-    per_layer = {"gemm_qkv": qkv_n * d, "gemm_o": d * d, "gemm_up": 2 * F * d, "gemm_down": d * F}
+    per_layer = {"gemm_qkv": qkv_n * d, "gemm_o": d * d, "gemm_o_norm": d * d, "gemm_up": 2 * F * d,
+                 "gemm_down": d * F, "gemm_down_norm": d * F}
     out = {k: 2 * v * cfg["n_layers"] for k, v in per_layer.items()}
     out["gemm_head"] = 2 * V * d
     return out
@@ -142,14 +143,14 @@ def main():
     ops = gemm_ops_per_token(cfg, kv_mode)
     nrows = ((n + chunk - 1) // chunk) * chunk
     kernels = {}
-    for name in ["prep", "embed_norm", "gemm_qkv", "attention", "gemm_o", "row_norm", "gemm_up", "gemm_down",
-                 "gemm_head", "cdf", "encode"]:
+    for name in ["prep", "embed_norm", "gemm_qkv", "attention", "gemm_o", "gemm_o_norm", "row_norm", "gemm_up",
+                 "gemm_down", "gemm_down_norm", "gemm_head", "cdf", "encode"]:
         launches, tot = model.kernel_stats(name)
         if launches:
             kernels[name] = {"launches": launches, "avg_ms": tot / launches, "ms_per_step": tot / args.steps}
     dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
     gemm_ms = sum(kernels[k]["ms_per_step"] for k in kernels if k.startswith("gemm"))
-    gemm_tops = sum(ops.values()) * nrows / (gemm_ms / 1000.0) / 1e12 if gemm_ms else 0.0
+    gemm_tops = sum(ops[k] for k in kernels if k in ops) * nrows / (gemm_ms / 1000.0) / 1e12 if gemm_ms else 0.0
     if dom.startswith("gemm"):
         per_launch = ops[dom] * nrows / (kernels[dom]["launches"] / args.steps)
         ach = per_launch / (kernels[dom]["avg_ms"] / 1000.0) / 1e12
@@ -188,8 +189,8 @@ def main():
         if text is not None and tokenizer.decode_bytes(back) != text:
             raise SystemExit("detokenized output differs from the input text")
         dk = {}
-        for name in ["dec_init", "dec_prep", "embed_norm", "gemm_qkv", "attn_decode", "gemm_o", "row_norm",
-                     "gemm_up", "gemm_down", "gemm_head", "cdf_decode"]:
+        for name in ["dec_init", "dec_prep", "embed_norm", "gemm_qkv", "attn_decode", "gemm_o", "gemm_o_norm",
+                     "row_norm", "gemm_up", "gemm_down", "gemm_down_norm", "gemm_head", "cdf_decode"]:
             launches, tot = model.kernel_stats(name)
             if launches:
                 dk[name] = {"ms": round(tot, 3), "launches": launches}

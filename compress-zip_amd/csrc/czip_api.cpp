@@ -33,7 +33,8 @@ struct DevLayer {
 // Requantization parameters of a GEMM launch (model.rs:280-300).  The fast
 // path multiplies in f64, exact while |acc * mult| < 2^53: |acc| <= K * 127 * 128
 // < 2^27 for K <= 8192, so |mult| < 2^26 suffices.
-void set_requant(GemmArgs& g, int mult, int shift) {
+template <class G>
+void set_requant(G& g, int mult, int shift) {
     g.mult = mult;
     g.shift = shift;
     const long long am = mult < 0 ? -(long long)mult : (long long)mult;
@@ -66,6 +67,7 @@ struct czip_ctx {
     hipStream_t stream = nullptr;
     czip_model_desc cfg{};
     int KH = 1;  // cached KV heads per layer
+    bool rn_fused = false;  // residual + norms fused into the row GEMM (gemm_rn_supported(d_model))
     std::vector<void*> allocs;
     int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr;
     uint16_t* lut = nullptr;
@@ -97,7 +99,7 @@ struct czip_job {
     uint32_t *inp = nullptr, *tgt = nullptr, *lohi = nullptr, *lohi_all = nullptr;
     int32_t* lens = nullptr;      // lengths of the chunks of the current sub-batch
     int32_t* lens_all = nullptr;  // lengths of every chunk of the job
-    int32_t* x = nullptr;
+    int16_t* x = nullptr;  // residual stream (|x| <= 127 * (2 * n_layers + 1) < 2^15)
     int8_t *xn = nullptr, *q8 = nullptr, *kc = nullptr, *vc = nullptr, *attn = nullptr, *y8 = nullptr, *r8 = nullptr;
     int32_t* logits = nullptr;
     // decompress
@@ -196,7 +198,8 @@ czip_status check_config(czip_ctx* c, const czip_model_desc& w) {
     if (w.d_ff < 32 || w.d_ff % 32 != 0) return fail(c, CZIP_E_CONFIG, "d_ff must be a multiple of 32");
     if (w.d_ff % 64 != 0) return fail(c, CZIP_E_CONFIG, "d_ff must be a multiple of 64");
     if (w.vocab < 2 || w.vocab > 8192 || w.vocab % 64 != 0) return fail(c, CZIP_E_CONFIG, "vocab must be a multiple of 64 in [64, 8192]");
-    if (w.n_layers < 1) return fail(c, CZIP_E_CONFIG, "n_layers must be >= 1");
+    if (w.n_layers < 1 || w.n_layers > 128)
+        return fail(c, CZIP_E_CONFIG, "n_layers must be in [1, 128] (the residual stream is held in int16)");
     if (w.n_kv_heads < 1) return fail(c, CZIP_E_CONFIG, "n_kv_heads must be >= 1");
     if (w.kv_mode == CZIP_KV_RUST_COMPAT) {
         if (!(w.n_heads == 4 || w.n_heads == 6 || w.n_heads == 8))
@@ -271,6 +274,7 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return CZIP_E_HIP;
     const size_t d = (size_t)w->d_model, F = (size_t)w->d_ff, V = (size_t)w->vocab, G = (size_t)w->n_kv_heads;
     c->KH = w->kv_mode == CZIP_KV_GQA ? w->n_kv_heads : 1;
+    c->rn_fused = gemm_rn_supported(w->d_model) && getenv("CZIP_UNFUSED_NORM") == nullptr;
     czip_ctx* C = c.get();
 #define UP(dst, src, n) if ((rc = upload(C, &dst, src, n))) return rc;
     UP(c->embed, w->embed, V * d)
@@ -348,7 +352,7 @@ int pad64(int T) { return (T + 63) & ~63; }
 
 size_t row_bytes(const czip_ctx* c) {
     const size_t d = (size_t)c->cfg.d_model, F = (size_t)c->cfg.d_ff, V = (size_t)c->cfg.vocab;
-    return 4 * d /*x*/ + 5 * d /*xn q8 attn y8*/ + F /*r8*/ + 4 * V /*logits*/ + 8 /*lohi*/ + 8 /*inp tgt*/ +
+    return 2 * d /*x*/ + 5 * d /*xn q8 attn y8*/ + F /*r8*/ + 4 * V /*logits*/ + 8 /*lohi*/ + 8 /*inp tgt*/ +
            2 * (size_t)c->KH * 64 /*kv*/ + 64;
 }
 
@@ -379,6 +383,52 @@ int pick_batch_chunks(const czip_ctx* c, int64_t nchunks, int T) {
     return (int)bc;
 }
 
+// Output projection, residual + norms and FFN of layer l on M rows whose
+// attention output is j->attn (model.rs:423-468); leaves the next layer's (or
+// the final) normalized input in j->xn and the residual stream in j->x.  With
+// the row GEMM the projection outputs stay on chip; layer 0 re-reads its
+// residual input from the embedding rows of j->inp.
+void post_attention(czip_ctx* c, czip_job* j, int l, int M) {
+    const int d = c->cfg.d_model, F = c->cfg.d_ff;
+    hipStream_t s = c->stream;
+    const DevLayer& L = c->layers[(size_t)l];
+    const bool last = l + 1 == c->cfg.n_layers;
+    const int8_t* next = last ? c->final_norm : c->layers[(size_t)l + 1].attn_norm;
+    if (c->rn_fused) {
+        RowGemmArgs o{};
+        o.A = j->attn; o.W = L.out_w; o.M = M; o.K = d; o.d = d;
+        set_requant(o, L.out_mult, L.out_shift);
+        o.w1 = L.ffn_norm; o.w2 = L.post_attn_norm;
+        o.x_in = l == 0 ? nullptr : j->x; o.tok = j->inp; o.embed = c->embed;
+        o.x_out = j->x; o.xn = j->xn;
+        { Timed t(c, "gemm_o_norm"); launch_gemm_rn(o, s); }
+    } else {
+        GemmArgs o{};
+        o.A = j->attn; o.W = L.out_w; o.M = M; o.N = d; o.K = d; o.out8 = j->y8; o.ldo = d;
+        set_requant(o, L.out_mult, L.out_shift);
+        { Timed t(c, "gemm_o"); launch_gemm(o, EPI_REQ, s); }
+        { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.ffn_norm, L.post_attn_norm, M, d, j->xn, s); }
+    }
+    GemmArgs u{};
+    u.A = j->xn; u.W = L.up_w; u.M = M; u.N = 2 * F; u.K = d; u.out8 = j->r8; u.ldo = F;
+    set_requant(u, L.up_mult, L.up_shift);
+    { Timed t(c, "gemm_up"); launch_gemm(u, EPI_REGLU, s); }
+    if (c->rn_fused) {
+        RowGemmArgs dn{};
+        dn.A = j->r8; dn.W = L.down_w; dn.M = M; dn.K = F; dn.d = d;
+        set_requant(dn, L.down_mult, L.down_shift);
+        dn.w1 = L.post_ffn_norm; dn.w2 = next;
+        dn.x_in = j->x; dn.x_out = last ? nullptr : j->x; dn.xn = j->xn;
+        { Timed t(c, "gemm_down_norm"); launch_gemm_rn(dn, s); }
+    } else {
+        GemmArgs dn{};
+        dn.A = j->r8; dn.W = L.down_w; dn.M = M; dn.N = d; dn.K = F; dn.out8 = j->y8; dn.ldo = d;
+        set_requant(dn, L.down_mult, L.down_shift);
+        { Timed t(c, "gemm_down"); launch_gemm(dn, EPI_REQ, s); }
+        { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.post_ffn_norm, next, M, d, j->xn, s); }
+    }
+}
+
 // Run every layer on rows [0, nb*T) whose inputs are j->inp / j->lens; leaves
 // logits in j->logits.  (model.rs:362-480 as batched launches)
 czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T) {
@@ -387,7 +437,7 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T) {
     hipStream_t s = c->stream;
     {
         Timed t(c, "embed_norm");
-        launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, M, d, j->x, j->xn, s);
+        launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, M, d, c->rn_fused ? nullptr : j->x, j->xn, s);
     }
     for (int l = 0; l < c->cfg.n_layers; l++) {
         const DevLayer& L = c->layers[(size_t)l];
@@ -403,21 +453,7 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T) {
         a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
         a.general = L.attn_general;
         { Timed t(c, "attention"); launch_attention(a, nb, s); }
-        GemmArgs o{};
-        o.A = j->attn; o.W = L.out_w; o.M = M; o.N = d; o.K = d; o.out8 = j->y8; o.ldo = d;
-        set_requant(o, L.out_mult, L.out_shift);
-        { Timed t(c, "gemm_o"); launch_gemm(o, EPI_REQ, s); }
-        { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.ffn_norm, L.post_attn_norm, M, d, j->xn, s); }
-        GemmArgs u{};
-        u.A = j->xn; u.W = L.up_w; u.M = M; u.N = 2 * F; u.K = d; u.out8 = j->r8; u.ldo = F;
-        set_requant(u, L.up_mult, L.up_shift);
-        { Timed t(c, "gemm_up"); launch_gemm(u, EPI_REGLU, s); }
-        GemmArgs dn{};
-        dn.A = j->r8; dn.W = L.down_w; dn.M = M; dn.N = d; dn.K = F; dn.out8 = j->y8; dn.ldo = d;
-        set_requant(dn, L.down_mult, L.down_shift);
-        { Timed t(c, "gemm_down"); launch_gemm(dn, EPI_REQ, s); }
-        const int8_t* next = (l + 1 < c->cfg.n_layers) ? c->layers[(size_t)l + 1].attn_norm : c->final_norm;
-        { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.post_ffn_norm, next, M, d, j->xn, s); }
+        post_attention(c, j, l, M);
     }
     GemmArgs h{};
     h.A = j->xn; h.W = c->head_w; h.M = M; h.N = V; h.K = d; h.out32 = j->logits; h.ldo = V;
@@ -724,7 +760,7 @@ static czip_status run_decompress(czip_job* j) {
         { Timed t(c, "dec_init"); launch_dec_init(st, ds, S, s); }
         for (int p = 0; p < steps; p++) {
             { Timed t(c, "dec_prep"); launch_dec_prep(ds, S, p, j->inp, s); }
-            { Timed t(c, "embed_norm"); launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, S, d, j->x, j->xn, s); }
+            { Timed t(c, "embed_norm"); launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, S, d, c->rn_fused ? nullptr : j->x, j->xn, s); }
             for (int l = 0; l < c->cfg.n_layers; l++) {
                 const DevLayer& L = c->layers[(size_t)l];
                 int8_t* kc = j->kc + (size_t)l * layer_kv;
@@ -741,21 +777,7 @@ static czip_status run_decompress(czip_job* j) {
                 a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;
                 a.general = L.attn_general;
                 { Timed t(c, "attn_decode"); launch_attn_decode(a, S, p, s); }
-                GemmArgs o{};
-                o.A = j->attn; o.W = L.out_w; o.M = S; o.N = d; o.K = d; o.out8 = j->y8; o.ldo = d;
-                set_requant(o, L.out_mult, L.out_shift);
-                { Timed t(c, "gemm_o"); launch_gemm(o, EPI_REQ, s); }
-                { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.ffn_norm, L.post_attn_norm, S, d, j->xn, s); }
-                GemmArgs u{};
-                u.A = j->xn; u.W = L.up_w; u.M = S; u.N = 2 * F; u.K = d; u.out8 = j->r8; u.ldo = F;
-                set_requant(u, L.up_mult, L.up_shift);
-                { Timed t(c, "gemm_up"); launch_gemm(u, EPI_REGLU, s); }
-                GemmArgs dn{};
-                dn.A = j->r8; dn.W = L.down_w; dn.M = S; dn.N = d; dn.K = F; dn.out8 = j->y8; dn.ldo = d;
-                set_requant(dn, L.down_mult, L.down_shift);
-                { Timed t(c, "gemm_down"); launch_gemm(dn, EPI_REQ, s); }
-                const int8_t* next = (l + 1 < c->cfg.n_layers) ? c->layers[(size_t)l + 1].attn_norm : c->final_norm;
-                { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.post_ffn_norm, next, S, d, j->xn, s); }
+                post_attention(c, j, l, S);
             }
             GemmArgs hd{};
             hd.A = j->xn; hd.W = c->head_w; hd.M = S; hd.N = V; hd.K = d; hd.out32 = j->logits; hd.ldo = V;

@@ -100,6 +100,25 @@ __device__ __forceinline__ int inv_rms_q15(int mean_sq) {
     return (int)(inv < 1u ? 1u : (inv > 32768u ? 32768u : inv));
 }
 
+// inv_rms_q15 for mean_sq in [1, 2^16): isqrt by f64 sqrt with an exact
+// integer correction, the RNE quotient by an f64 estimate with an exact
+// remainder test (8388608 / s with s in [256, 2^16)).  Same results as
+// inv_rms_q15 on that range.
+__device__ __forceinline__ int inv_rms_q15_fast(int mean_sq) {
+    const unsigned x = (unsigned)(mean_sq > 0 ? mean_sq : 1) << 16;
+    unsigned long long r = (unsigned long long)__builtin_sqrt((double)x);
+    if (r * r > x) r--;
+    if ((r + 1) * (r + 1) <= x) r++;
+    const unsigned d = (unsigned)r;
+    unsigned q = (unsigned)(8388608.0 / (double)d);
+    int rem = (int)(8388608u - q * d);
+    if (rem < 0) { q--; rem += (int)d; }
+    if (rem >= (int)d) { q++; rem -= (int)d; }
+    const unsigned tr = (unsigned)rem << 1;
+    const unsigned inv = tr > d ? q + 1 : (tr == d ? q + (q & 1u) : q);
+    return (int)(inv < 1u ? 1u : (inv > 32768u ? 32768u : inv));
+}
+
 // lut.rs:213-235 / softmax_cdf.rs:55-77
 __device__ __forceinline__ unsigned exp_q16(int diff, const uint16_t* lut, unsigned coef) {
     if (diff >= 0) return 65535u;

@@ -44,13 +44,17 @@ __device__ __forceinline__ void store_tile(const TileRegs& t, int8_t* lds, int t
 // model.rs:280-300.  Fast path: |v * mult| < 2^53, so v * mult * 2^-shift is
 // exact in f64 and rint rounds half to even like sra_rne_tte_s64_to_s32.
 template <bool FAST>
-__device__ __forceinline__ int rq(int v, const GemmArgs& a) {
+__device__ __forceinline__ int rq(int v, double scale, int mult, int shift) {
     if (FAST) {
-        double x = __builtin_rint((double)v * a.rq_scale);
+        double x = __builtin_rint((double)v * scale);
         x = fmin(fmax(x, -127.0), 127.0);
         return (int)x;
     }
-    return requant(v, a.mult, a.shift);
+    return requant(v, mult, shift);
+}
+template <bool FAST>
+__device__ __forceinline__ int rq(int v, const GemmArgs& a) {
+    return rq<FAST>(v, a.rq_scale, a.mult, a.shift);
 }
 
 __device__ __forceinline__ unsigned pack4i(int a, int b, int c, int d) {
@@ -206,6 +210,200 @@ void launch_gemm(const GemmArgs& a, int epi, hipStream_t s) {
         case EPI_REQ: launch_epi<EPI_REQ>(a, grid, s); break;
         case EPI_QKV: launch_epi<EPI_QKV>(a, grid, s); break;
         default: launch_epi<EPI_REGLU>(a, grid, s); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Row GEMM: a workgroup owns 64 rows and all d output columns, so the
+// requantization, both RMSNorms and the residual add run in its epilogue and
+// the projection output never leaves the chip.  NW waves split the columns
+// (CT 16-wide tiles each, d = NW * CT * 16); the 64 x 64 A tile of each K step
+// goes through double-buffered LDS, and each wave streams its own W columns
+// straight into registers (no W element is used by two waves).
+// ---------------------------------------------------------------------------
+constexpr int RBM = 64;
+
+__device__ __forceinline__ void unpack4s(unsigned w, int* o) {
+    o[0] = (int)(int8_t)(w & 0xFF);
+    o[1] = (int)(int8_t)((w >> 8) & 0xFF);
+    o[2] = (int)(int8_t)((w >> 16) & 0xFF);
+    o[3] = (int)(int8_t)(w >> 24);
+}
+
+// rmsnorm.rs:40-75 for one element: clamp(sra_rne((x * w) * inv, 15)), |x * w * inv| < 2^30
+__device__ __forceinline__ int rms_el(int x, int w, int inv) { return clamp127(rne_shr(x * w * inv, 15)); }
+
+template <int NW, int CT, bool FAST>
+__global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) int8_t As[2][RBM * LDSK];
+    __shared__ unsigned red[NW][RBM];
+    __shared__ int inv_s[RBM];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int m0 = blockIdx.x * RBM;
+    const int nb = wave * CT * 16;  // first output column of this wave
+    const int lr = lane & 15, lk = (lane >> 4) * 16, c4 = (lane >> 4) * 4;
+    const int nk = a.K / BK;
+
+    v4i acc[4][CT];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int t = 0; t < CT; t++) acc[i][t] = (v4i){0, 0, 0, 0};
+
+    // A tile of a K step: 64 rows x 64 bytes, 16 bytes per thread of the first 256
+    const int ar = tid >> 2, ac = (tid & 3) * 16;
+    int4 ra = make_int4(0, 0, 0, 0);
+    auto fetch_a = [&](int k0) {
+        ra = make_int4(0, 0, 0, 0);
+        if (tid < 256 && m0 + ar < a.M) ra = *(const int4*)(a.A + (size_t)(m0 + ar) * a.K + k0 + ac);
+    };
+    auto store_a = [&](int buf) {
+        if (tid < 256) *(int4*)(As[buf] + ar * LDSK + ac) = ra;
+    };
+    v4i wf[CT];
+    auto fetch_w = [&](int k0) {
+#pragma unroll
+        for (int t = 0; t < CT; t++) wf[t] = *(const v4i*)(a.W + (size_t)(nb + t * 16 + lr) * a.K + k0 + lk);
+    };
+    fetch_a(0);
+    fetch_w(0);
+    store_a(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        v4i wc[CT];
+#pragma unroll
+        for (int t = 0; t < CT; t++) wc[t] = wf[t];
+        if (kt + 1 < nk) {
+            fetch_a((kt + 1) * BK);
+            fetch_w((kt + 1) * BK);
+        }
+        v4i af[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[cur] + (i * 16 + lr) * LDSK + lk);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int t = 0; t < CT; t++) acc[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wc[t], af[i], acc[i][t], 0, 0, 0);
+        if (kt + 1 < nk) store_a(cur ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue.  Lane holds columns nb + 16 t + c4 .. +3 of rows m0 + 16 i + lr.
+    // 1. y = requant(acc); row sums of y^2
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        unsigned ss = 0;
+#pragma unroll
+        for (int t = 0; t < CT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int y = rq<FAST>(acc[i][t][r], a.rq_scale, a.mult, a.shift);
+                acc[i][t][r] = y;
+                ss += (unsigned)(y * y);
+            }
+        ss += (unsigned)__shfl_xor((int)ss, 16, 64);
+        ss += (unsigned)__shfl_xor((int)ss, 32, 64);
+        if (lane < 16) red[wave][i * 16 + lane] = ss;
+    }
+    __syncthreads();
+    auto row_inv = [&]() {
+        if (wave == 0) {
+            unsigned s = 0;
+#pragma unroll
+            for (int w = 0; w < NW; w++) s += red[w][lane];
+            int mean_sq = (int)(s / (unsigned)a.d) + 1;  // eps_scaled = 1 (rmsnorm.rs:80-83)
+            inv_s[lane] = inv_rms_q15_fast(mean_sq);  // mean_sq <= 127^2 + 1
+        }
+        __syncthreads();
+    };
+    row_inv();
+    // 2. x = x_in + rmsnorm(y, w1); keep clamp(x); row sums of clamp(x)^2
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = m0 + i * 16 + lr;
+        const bool live = row < a.M;
+        const int inv = inv_s[i * 16 + lr];
+        const int8_t* erow = nullptr;
+        if (!a.x_in && live) erow = a.embed + (size_t)a.tok[row] * a.d;
+        unsigned ss = 0;
+#pragma unroll
+        for (int t = 0; t < CT; t++) {
+            const int n = nb + t * 16 + c4;
+            int w1v[4], xo[4] = {0, 0, 0, 0};
+            unpack4s(*(const unsigned*)(a.w1 + n), w1v);
+            if (live) {
+                if (a.x_in) {
+                    const uint2 xv = *(const uint2*)(a.x_in + (size_t)row * a.d + n);
+                    xo[0] = (int16_t)(xv.x & 0xFFFFu); xo[1] = (int16_t)(xv.x >> 16);
+                    xo[2] = (int16_t)(xv.y & 0xFFFFu); xo[3] = (int16_t)(xv.y >> 16);
+                } else {
+                    unpack4s(*(const unsigned*)(erow + n), xo);
+                }
+            }
+            int xnw[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                xnw[r] = xo[r] + rms_el(acc[i][t][r], w1v[r], inv);
+                const int xc = clamp127(xnw[r]);
+                acc[i][t][r] = xc;
+                ss += (unsigned)(xc * xc);
+            }
+            if (a.x_out && live)
+                *(uint2*)(a.x_out + (size_t)row * a.d + n) = make_uint2(((unsigned)xnw[0] & 0xFFFFu) | ((unsigned)xnw[1] << 16),
+                                                                        ((unsigned)xnw[2] & 0xFFFFu) | ((unsigned)xnw[3] << 16));
+        }
+        ss += (unsigned)__shfl_xor((int)ss, 16, 64);
+        ss += (unsigned)__shfl_xor((int)ss, 32, 64);
+        if (lane < 16) red[wave][i * 16 + lane] = ss;
+    }
+    __syncthreads();
+    row_inv();
+    // 3. xn = rmsnorm(clamp(x), w2)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = m0 + i * 16 + lr;
+        if (row >= a.M) continue;
+        const int inv = inv_s[i * 16 + lr];
+#pragma unroll
+        for (int t = 0; t < CT; t++) {
+            const int n = nb + t * 16 + c4;
+            int w2v[4];
+            unpack4s(*(const unsigned*)(a.w2 + n), w2v);
+            *(unsigned*)(a.xn + (size_t)row * a.d + n) =
+                pack4i(rms_el(acc[i][t][0], w2v[0], inv), rms_el(acc[i][t][1], w2v[1], inv),
+                       rms_el(acc[i][t][2], w2v[2], inv), rms_el(acc[i][t][3], w2v[3], inv));
+        }
+    }
+}
+
+bool gemm_rn_supported(int d) {
+    const int h = d / 64;
+    return d % 64 == 0 && ((h >= 4 && h <= 8) || h == 10 || h == 12 || h == 14 || h == 16);
+}
+
+template <int NW, int CT>
+static void launch_rn(const RowGemmArgs& a, hipStream_t s) {
+    dim3 grid((unsigned)((a.M + RBM - 1) / RBM));
+    if (a.rq_fast)
+        hipLaunchKernelGGL((k_gemm_rn<NW, CT, true>), grid, dim3(64 * NW), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_gemm_rn<NW, CT, false>), grid, dim3(64 * NW), 0, s, a);
+}
+
+// d = 64 h columns over NW waves of CT 16-wide tiles: 8 waves where h is even
+// (few accumulators per wave, many waves to hide the W stream's latency)
+void launch_gemm_rn(const RowGemmArgs& a, hipStream_t s) {
+    switch (a.d / 64) {
+        case 4: launch_rn<8, 2>(a, s); break;
+        case 5: launch_rn<4, 5>(a, s); break;
+        case 6: launch_rn<8, 3>(a, s); break;
+        case 7: launch_rn<4, 7>(a, s); break;
+        case 8: launch_rn<8, 4>(a, s); break;
+        case 10: launch_rn<8, 5>(a, s); break;
+        case 12: launch_rn<8, 6>(a, s); break;
+        case 14: launch_rn<8, 7>(a, s); break;
+        default: launch_rn<16, 4>(a, s); break;
     }
 }
 

@@ -49,11 +49,34 @@ struct AttnArgs {
     int general;              // 1: scores may reach 2^30 or lut[0] != 65535 (wrapping score differences)
 };
 
+// GEMM over full rows (N = d) with the residual + RMSNorm epilogue
+// (model.rs:424-439 after the output projection, 459-468 + 384-385 / 473-474
+// after the down projection):
+//   y = requant(A W^T); x = x_in + rmsnorm(y, w1); xn = rmsnorm(clamp(x), w2)
+struct RowGemmArgs {
+    const int8_t* A;      // [M, K]
+    const int8_t* W;      // [d, K]
+    int M, K, d;
+    int mult, shift;
+    double rq_scale;
+    int rq_fast;
+    const int8_t* w1;      // norm of the projection output
+    const int8_t* w2;      // norm of the clamped residual
+    const int16_t* x_in;   // residual stream [M, d]; nullptr: the embedding rows of tok
+    const uint32_t* tok;
+    const int8_t* embed;
+    int16_t* x_out;        // [M, d] or nullptr (not needed after the last layer)
+    int8_t* xn;            // [M, d]
+};
+bool gemm_rn_supported(int d);
+void launch_gemm_rn(const RowGemmArgs& a, hipStream_t s);
+
 void launch_prep_chunks(const uint32_t* toks, int64_t n_tokens, int64_t chunk0, int nb, int T,
                         uint32_t* inp, uint32_t* tgt, int32_t* lens, hipStream_t s);
+// x may be nullptr (the residual stream is re-read from the embedding rows)
 void launch_embed_norm(const uint32_t* inp, const int8_t* embed, const int8_t* w, int M, int d,
-                       int32_t* x, int8_t* xn, hipStream_t s);
-void launch_resid_norm(int32_t* x, const int8_t* y8, const int8_t* w1, const int8_t* w2, int M, int d,
+                       int16_t* x, int8_t* xn, hipStream_t s);
+void launch_resid_norm(int16_t* x, const int8_t* y8, const int8_t* w1, const int8_t* w2, int M, int d,
                        int8_t* xn, hipStream_t s);
 void launch_gemm(const GemmArgs& a, int epi, hipStream_t s);
 void launch_attention(const AttnArgs& a, int B, hipStream_t s);

@@ -165,6 +165,25 @@ def test_attention_general_path(amd, orc, tmp_path):
         _check_logits(gm, om, 192, [192, 77], 60 + sink, 1024)
 
 
+def test_unfused_norm_path(amd, orc, tmp_path, monkeypatch):
+    """The residual + RMSNorm row kernels that back the row GEMM where it has no
+    instance (three heads) or is switched off, in both passes."""
+    from czip_amd import synth
+    path = synth.write_random_model(str(tmp_path / "h3.czm"), d=192, n_layers=2, n_heads=3, n_kv=1, d_ff=256,
+                                    vocab=1024, ctx=128, seed=90)
+    gm, om = _model_pair(amd, orc, path, amd.KV_GQA)
+    _check_logits(gm, om, 128, [128, 60], 91, 1024)
+    monkeypatch.setenv("CZIP_UNFUSED_NORM", "1")
+    gm2 = amd.Model(amd.ModelWeights(MODEL_PATH))
+    lens = [64, 40]
+    toks = synth.zipf_ids(sum(lens), 1024, seed=92)
+    _say("compress shipped, unfused norms")
+    ref = orc.Model.from_file(MODEL_PATH).compress_many(toks, 64, threads=2)
+    assert gm2.compress_chunks(toks, 64) == ref
+    out = gm2.decompress_chunks(ref, lens)
+    assert np.array_equal(out, toks)
+
+
 def test_requant_general_path(amd, orc, tmp_path):
     """Requantization outside the GEMMs' f64 fast path (|mult| >= 2^26, negative
     multipliers, shift <= 0) against the oracle."""
