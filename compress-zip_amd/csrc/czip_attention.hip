@@ -13,20 +13,20 @@ namespace czip {
 // order; only the rescales must be applied in key order.
 //
 // One workgroup = one chunk, one head, 64 query rows (4 waves x 16 rows).
-// Per 64-key tile each wave:
+// Per 64-key tile (the next tile's K and V^T are fetched into registers
+// meanwhile) each wave:
 //  1. forms S^T = K Q^T (int8 MFMA) and the score epilogue in f64, which is
 //     exact: |dot / 4 * mult| < 2^49;
 //  2. scans its rows' keys in order (a lane owns 16 consecutive keys of one
 //     row): running max, records, one exp per key.  A key's weight and, at a
 //     record, the rescale factor are both E(-|s - max before the key|);
-//  3. packs the (row, segment) pairs of its 16 rows densely into MFMA
-//     columns (a tile has ~2 records per row but up to 64), and for each
-//     group of 16 columns forms the segment sums O^T = V^T P^T on int8 MFMA.
-//     The 16-bit weights enter as two signed bytes: w - 32896 = 256*hi + lo,
-//     keys outside a column's segment carry w = 0, and 32896 * sum(v) is
-//     added back;
-//  4. walks each row's columns in order: rescale at the record, then add,
-//     with lanes = head dims for vacc and S in scalar registers.
+//  3. for each segment index j = 0..max records, forms the segment sums of
+//     all 16 rows at once, O_j^T = V^T P_j^T, on int8 MFMA.  The 16-bit
+//     weights enter as two signed bytes: w - 32896 = 256*hi + lo, keys outside
+//     segment j carry w = 0, and the constant 32896 * sum(v) is added back;
+//  4. hands O_j through LDS to a "lanes = head dims" layout and walks each
+//     row's own segments: rescale at the record, then add (rows with fewer
+//     records skip the pass with a scalar branch); S is kept with lanes = rows.
 // Scores are kept as s ^ 2^31 so that unsigned order is signed order; 0 is
 // INT32_MIN, the reference's "nothing seen yet".
 // ---------------------------------------------------------------------------
@@ -35,12 +35,11 @@ constexpr int KLD = 80;               // LDS row stride (bytes) of the K tile an
 constexpr unsigned WOFF = 32896;      // w - WOFF spans [-32896, 32639] = 256*[-128,127] + [-128,127]
 constexpr unsigned BIAS = 0x80000000u;
 constexpr int RS = 68;                // row stride (words) of the per-wave buffer: 16-byte accesses of 16 rows hit 64 banks
-constexpr int MAXCOL = 16 * 65;       // (row, segment) columns of a wave-tile: 16 rows x (64 records + 1)
 
 struct AttnWaveLds {
     unsigned buf[16][RS];    // scores [row][key]; then per pass: column sums [column][dim]
     uint16_t rec_e[16][64];  // rescale factor at record j+1 of row r (0: nothing to rescale)
-    uint16_t col[MAXCOL];    // column -> row | segment << 4
+    int nrec[16];            // records of each row in the tile
 };
 
 __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
@@ -77,10 +76,9 @@ __device__ __forceinline__ unsigned rescale_v(unsigned v, unsigned e) {
     return (unsigned)__mul24(vh, (int)e) + (t >> 16) + ((t >> 15) & 1u) + (unsigned)((int)v >> 31);
 }
 
-// S rescale at a record (attention.rs:246-250): (S * e + 0x8000) >> 16, with
-// S < 2^32 and e < 2^16
-__device__ __forceinline__ unsigned rescale_s(unsigned S, unsigned e) {
-    return (unsigned)(((unsigned long long)S * e + 0x8000ull) >> 16);
+// S rescale at a record (attention.rs:246-250): (S * e + 0x8000) >> 16
+__device__ __forceinline__ unsigned long long rescale_s64(unsigned long long S, unsigned e) {
+    return (S * e + 0x8000ull) >> 16;
 }
 
 // bytes of x equal to zero -> 0xFF, others -> 0x00 (exact per byte)
@@ -93,7 +91,7 @@ __device__ __forceinline__ unsigned zero_bytes_mask(unsigned x) {
 __device__ __forceinline__ unsigned pick(unsigned msk, unsigned a, unsigned b) { return (a & msk) | (b & ~msk); }
 
 template <bool GEN>
-__global__ __launch_bounds__(256, 3) void k_attention(AttnArgs a) {
+__global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     __shared__ unsigned lut32[256];
     __shared__ __attribute__((aligned(16))) int8_t Ks[64 * KLD];
     __shared__ __attribute__((aligned(16))) int8_t Vt[64 * KLD];
@@ -119,15 +117,13 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs a) {
     v4i qop = (v4i){0, 0, 0, 0};
     if (p < T) qop = *(const v4i*)(a.q + ((size_t)b * T + p) * D + h * 64 + grp * 16);
 
-    // state: running max m (biased) with lanes = rows (replicated over the 4
-    // lane groups); vacc with lanes = head dims (register index = row); the
-    // weight sums S of the 16 rows are wave-uniform (scalar registers).  S fits
-    // in 32 bits: S <= 65535 * (T + 1) < 2^32 for T <= 65535.
+    // state: running max m (biased) and weight sum S with lanes = rows
+    // (replicated over the 4 lane groups); vacc with lanes = head dims
+    // (register index = row)
     unsigned m = 0u;
-    unsigned Sr[16];
+    unsigned long long S = 0;
     unsigned vacc[16];
     for (int r = 0; r < 16; r++) vacc[r] = 0;
-    unsigned s_init = 0u;
     if (a.sink) {  // attention.rs:211-224: sink score is the initial max, weight E(0) = 65535
         const int* sk = (const int*)(a.sink + grp * 16);
         int dot = 0;
@@ -135,22 +131,28 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs a) {
         dot += __shfl_xor(dot, 16, 64);
         dot += __shfl_xor(dot, 32, 64);
         m = score_b<GEN>(dot, mscale);
-        s_init = 65535u;
+        S = 65535ull;
     }
-    for (int r = 0; r < 16; r++) Sr[r] = s_init;
 
     const int ntiles = (min(q0 + 63, len - 1)) / 64 + 1;
+    // K / V^T tile of 64 keys: thread -> row tid/4, 16 bytes; the next tile is
+    // fetched into registers while the current one is processed
+    const int ldr = tid >> 2, ldc = (tid & 3) * 16;
+    int4 kreg = make_int4(0, 0, 0, 0), vreg;
+    if (ldr < T) kreg = *(const int4*)(Kg + (size_t)ldr * 64 + ldc);
+    vreg = *(const int4*)(Vg + (size_t)ldr * a.TP + ldc);
     for (int kt = 0; kt < ntiles; kt++) {
         const int t0 = kt * 64;
         __syncthreads();
-        {
-            const int r = tid >> 2, c = (tid & 3) * 16;
-            int4 kv = make_int4(0, 0, 0, 0);
-            if (t0 + r < T) kv = *(const int4*)(Kg + (size_t)(t0 + r) * 64 + c);
-            *(int4*)(Ks + r * KLD + c) = kv;
-            *(int4*)(Vt + r * KLD + c) = *(const int4*)(Vg + (size_t)r * a.TP + t0 + c);
-        }
+        *(int4*)(Ks + ldr * KLD + ldc) = kreg;
+        *(int4*)(Vt + ldr * KLD + ldc) = vreg;
         __syncthreads();
+        if (kt + 1 < ntiles) {
+            const int t1 = t0 + 64;
+            kreg = make_int4(0, 0, 0, 0);
+            if (t1 + ldr < T) kreg = *(const int4*)(Kg + (size_t)(t1 + ldr) * 64 + ldc);
+            vreg = *(const int4*)(Vg + (size_t)ldr * a.TP + t1 + ldc);
+        }
         if (!wave_live || t0 > wave_last) continue;
 
         // 1. S^T = K Q^T, score epilogue, stored [row][key]
@@ -255,22 +257,11 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs a) {
         int nrow = nrec + __shfl_xor(nrec, 16, 64);
         nrow += __shfl_xor(nrow, 32, 64);
 
-        // 3. row r owns columns base_r .. base_r + nrow_r (segment j = column - base_r)
-        const int ncol = nrow + 1;
-        int incl = ncol;
+        // 3. segment j of every row in pass j (MFMA column = row): O_j^T = V^T P_j^T
+        if (grp == 0) W.nrec[row] = nrow;
+        int nmax = nrow;
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            const int t = __shfl_up(incl, o, 16);
-            if (row >= o) incl += t;
-        }
-        const int base = incl - ncol;
-        int bs[17];
-#pragma unroll
-        for (int r = 0; r < 16; r++) bs[r] = __builtin_amdgcn_readlane(base, r);
-        const int C = __builtin_amdgcn_readlane(incl, 15);
-        bs[16] = C;
-        for (int j = grp; j < ncol; j += 4) W.col[base + j] = (uint16_t)(row | (j << 4));
-
+        for (int o = 1; o < 16; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
         // A operand of the PV product: V^T row (head dim 16*db + lane % 16), keys 16*grp .. +16
         v4i vop[4];
 #pragma unroll
@@ -285,33 +276,30 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs a) {
             corr = (unsigned)cs * WOFF;
         }
         wave_lds_fence();
-
-        for (int c0 = 0; c0 < C; c0 += 16) {
-            // B operand of column c0 + lane % 16: its row's weights, masked to its segment
-            const int gc = c0 + row;
-            const unsigned info = gc < C ? (unsigned)W.col[gc] : 0xFE0u;  // segment 0xFE matches no key
-            const unsigned jcol = info >> 4;
-            // rescale factor at the column's record (0: segment 0, or nothing to rescale)
-            const unsigned ecol = (jcol >= 1u && jcol < 0xFEu) ? (unsigned)W.rec_e[info & 15u][jcol - 1u] : 0u;
-            const int src = (int)(info & 15u) + 16 * grp;
-            const unsigned jb = jcol * 0x01010101u;
+        int nr[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) nr[r] = __builtin_amdgcn_readfirstlane(W.nrec[r]);
+        for (int j = 0; j <= nmax; j++) {
+            const unsigned jb = (unsigned)j * 0x01010101u;
             v4i bh, bl;
             int sh = 0, sl = 0;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const unsigned hd = (unsigned)__shfl((int)hi_dw[i], src, 64);
-                const unsigned ld = (unsigned)__shfl((int)lo_dw[i], src, 64);
-                const unsigned sd = (unsigned)__shfl((int)sg_dw[i], src, 64);
-                const unsigned msk = zero_bytes_mask(sd ^ jb);
-                bh[i] = (int)pick(msk, hd, 0x80808080u);
-                bl[i] = (int)pick(msk, ld, 0x80808080u);
+                const unsigned msk = zero_bytes_mask(sg_dw[i] ^ jb);
+                bh[i] = (int)pick(msk, hi_dw[i], 0x80808080u);
+                bl[i] = (int)pick(msk, lo_dw[i], 0x80808080u);
                 sh = __builtin_amdgcn_sdot4(bh[i], 0x01010101, sh, false);
                 sl = __builtin_amdgcn_sdot4(bl[i], 0x01010101, sl, false);
             }
-            int sw = sh * 256 + sl;  // sum over this lane's 16 keys of (w - 32896)
+            int sw = sh * 256 + sl;  // sum over this lane's 16 keys of (w_j - 32896)
             sw += __shfl_xor(sw, 16, 64);
             sw += __shfl_xor(sw, 32, 64);
-            const unsigned swc = (unsigned)sw + 64u * WOFF;  // the column's weight sum
+            // 4a. S of this lane's row (lanes = rows): rescale at record j, then add segment j
+            if (j >= 1 && j <= nrow) {
+                const unsigned e = W.rec_e[row][j - 1];
+                if (e) S = rescale_s64(S, e);
+            }
+            S += (unsigned)sw + 64u * WOFF;
 #pragma unroll
             for (int db = 0; db < 4; db++) {
                 v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[db], bh, (v4i){0, 0, 0, 0}, 0, 0, 0);
@@ -320,36 +308,33 @@ __global__ __launch_bounds__(256, 3) void k_attention(AttnArgs a) {
                 *(int4*)&W.buf[row][db * 16 + grp * 4] = make_int4(acc[0], acc[1], acc[2], acc[3]);
             }
             wave_lds_fence();
-            // 4. the pass's columns, lanes = head dims: all 16 read at once, then
-            // walked row by row (the rows' columns are consecutive and in order)
+            // 4b. vacc (lanes = head dims): every row that has a segment j
             unsigned bv[16];
 #pragma unroll
-            for (int c = 0; c < 16; c++) bv[c] = W.buf[c][lane];
+            for (int r = 0; r < 16; r++) bv[r] = W.buf[r][lane];
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int lo = max(bs[r], c0), hi = min(bs[r + 1], c0 + 16);
-                for (int g2 = lo; g2 < hi; g2++) {
-                    const int c = g2 - c0;
-                    const unsigned e = (unsigned)__builtin_amdgcn_readlane((int)ecol, c);
-                    const unsigned swv = (unsigned)__builtin_amdgcn_readlane((int)swc, c);
-                    if (e) {
-                        vacc[r] = rescale_v(vacc[r], e);
-                        Sr[r] = rescale_s(Sr[r], e);
+                if (j <= nr[r]) {
+                    if (j >= 1) {
+                        const unsigned e = (unsigned)__builtin_amdgcn_readfirstlane(W.rec_e[r][j - 1]);
+                        if (e) vacc[r] = rescale_v(vacc[r], e);
                     }
-                    vacc[r] += bv[c] + corr;
-                    Sr[r] += swv;
+                    vacc[r] += bv[r] + corr;
                 }
             }
             wave_lds_fence();
         }
     }
     if (!wave_live) return;
-    // normalize (attention.rs:278-285): lane = head dim
+    // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r
 #pragma unroll
     for (int r = 0; r < 16; r++) {
+        const unsigned slo = (unsigned)__shfl((int)(unsigned)S, r, 64);
+        const unsigned shi = (unsigned)__shfl((int)(unsigned)(S >> 32), r, 64);
         const int pr = wrow0 + r;
         if (pr < len) {
-            const unsigned long long den = Sr[r] == 0u ? 1ull : (unsigned long long)Sr[r];
+            const unsigned long long Sr = ((unsigned long long)shi << 32) | slo;
+            const unsigned long long den = Sr == 0 ? 1ull : Sr;
             a.out[((size_t)b * T + pr) * D + h * 64 + lane] = (int8_t)clamp127(div_rne_s32_u64((int)vacc[r], den));
         }
     }
