@@ -59,6 +59,7 @@ def gemm_ops_per_token(cfg, kv_mode):
                  "gemm_down": d * F, "gemm_down_norm": d * F}
     out = {k: 2 * v * cfg["n_layers"] for k, v in per_layer.items()}
     out["gemm_head"] = 2 * V * d
+    out["head_cdf"] = 2 * V * d
     return out
 
 
@@ -144,12 +145,12 @@ def main():
     nrows = ((n + chunk - 1) // chunk) * chunk
     kernels = {}
     for name in ["prep", "embed_norm", "gemm_qkv", "attention", "gemm_o", "gemm_o_norm", "row_norm", "gemm_up",
-                 "gemm_down", "gemm_down_norm", "gemm_head", "cdf", "encode"]:
+                 "gemm_down", "gemm_down_norm", "gemm_head", "cdf", "head_cdf", "encode"]:
         launches, tot = model.kernel_stats(name)
         if launches:
             kernels[name] = {"launches": launches, "avg_ms": tot / launches, "ms_per_step": tot / args.steps}
     dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
-    gemm_ms = sum(kernels[k]["ms_per_step"] for k in kernels if k.startswith("gemm"))
+    gemm_ms = sum(kernels[k]["ms_per_step"] for k in kernels if k in ops)
     gemm_tops = sum(ops[k] for k in kernels if k in ops) * nrows / (gemm_ms / 1000.0) / 1e12 if gemm_ms else 0.0
     if dom.startswith("gemm"):
         per_launch = ops[dom] * nrows / (kernels[dom]["launches"] / args.steps)

@@ -68,6 +68,7 @@ struct czip_ctx {
     czip_model_desc cfg{};
     int KH = 1;  // cached KV heads per layer
     bool rn_fused = false;  // residual + norms fused into the row GEMM (gemm_rn_supported(d_model))
+    bool head_fused = false;  // compress: LM head fused with the coder interval stage (head_cdf_supported(vocab))
     std::vector<void*> allocs;
     int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr;
     uint16_t* lut = nullptr;
@@ -275,6 +276,7 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
     const size_t d = (size_t)w->d_model, F = (size_t)w->d_ff, V = (size_t)w->vocab, G = (size_t)w->n_kv_heads;
     c->KH = w->kv_mode == CZIP_KV_GQA ? w->n_kv_heads : 1;
     c->rn_fused = gemm_rn_supported(w->d_model) && getenv("CZIP_UNFUSED_NORM") == nullptr;
+    c->head_fused = head_cdf_supported(w->vocab) && getenv("CZIP_UNFUSED_HEAD") == nullptr;
     czip_ctx* C = c.get();
 #define UP(dst, src, n) if ((rc = upload(C, &dst, src, n))) return rc;
     UP(c->embed, w->embed, V * d)
@@ -350,13 +352,15 @@ namespace {
 
 int pad64(int T) { return (T + 63) & ~63; }
 
-size_t row_bytes(const czip_ctx* c) {
+// device bytes per token row of a forward batch (logits: the int32 logits are
+// materialized, i.e. the head is not fused with the coder interval stage)
+size_t row_bytes(const czip_ctx* c, bool logits = true) {
     const size_t d = (size_t)c->cfg.d_model, F = (size_t)c->cfg.d_ff, V = (size_t)c->cfg.vocab;
-    return 2 * d /*x*/ + 5 * d /*xn q8 attn y8*/ + F /*r8*/ + 4 * V /*logits*/ + 8 /*lohi*/ + 8 /*inp tgt*/ +
+    return 2 * d /*x*/ + 5 * d /*xn q8 attn y8*/ + F /*r8*/ + (logits ? 4 * V : 0) + 8 /*lohi*/ + 8 /*inp tgt*/ +
            2 * (size_t)c->KH * 64 /*kv*/ + 64;
 }
 
-czip_status alloc_scratch(czip_ctx* c, czip_job* j, int BC, int T) {
+czip_status alloc_scratch(czip_ctx* c, czip_job* j, int BC, int T, bool logits = true) {
     const size_t M = (size_t)BC * T;
     const size_t d = (size_t)c->cfg.d_model, F = (size_t)c->cfg.d_ff, V = (size_t)c->cfg.vocab;
     czip_status rc;
@@ -370,14 +374,14 @@ czip_status alloc_scratch(czip_ctx* c, czip_job* j, int BC, int T) {
     if ((rc = dalloc(c, j->allocs, &j->r8, M * F))) return rc;
     if ((rc = dalloc(c, j->allocs, &j->kc, M * (size_t)c->KH * 64))) return rc;
     if ((rc = dalloc(c, j->allocs, &j->vc, (size_t)BC * pad64(T) * (size_t)c->KH * 64))) return rc;
-    if ((rc = dalloc(c, j->allocs, &j->logits, M * V))) return rc;
+    if (logits && (rc = dalloc(c, j->allocs, &j->logits, M * V))) return rc;
     return CZIP_OK;
 }
 
-int pick_batch_chunks(const czip_ctx* c, int64_t nchunks, int T) {
+int pick_batch_chunks(const czip_ctx* c, int64_t nchunks, int T, bool logits = true) {
     double gb = 16.0;
     if (const char* s = getenv("CZIP_SCRATCH_GB")) gb = atof(s);
-    double per_chunk = (double)row_bytes(c) * T;
+    double per_chunk = (double)row_bytes(c, logits) * T;
     int64_t bc = (int64_t)(gb * 1e9 / per_chunk);
     bc = std::max<int64_t>(1, std::min<int64_t>(bc, nchunks));
     return (int)bc;
@@ -430,8 +434,9 @@ void post_attention(czip_ctx* c, czip_job* j, int l, int M) {
 }
 
 // Run every layer on rows [0, nb*T) whose inputs are j->inp / j->lens; leaves
-// logits in j->logits.  (model.rs:362-480 as batched launches)
-czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T) {
+// logits in j->logits (head), else the final-normalized rows in j->xn.
+// (model.rs:362-480 as batched launches)
+czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T, bool head = true) {
     const int M = nb * T;
     const int d = c->cfg.d_model, F = c->cfg.d_ff, V = c->cfg.vocab, H = c->cfg.n_heads;
     hipStream_t s = c->stream;
@@ -455,9 +460,12 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T) {
         { Timed t(c, "attention"); launch_attention(a, nb, s); }
         post_attention(c, j, l, M);
     }
-    GemmArgs h{};
-    h.A = j->xn; h.W = c->head_w; h.M = M; h.N = V; h.K = d; h.out32 = j->logits; h.ldo = V;
-    { Timed t(c, "gemm_head"); launch_gemm(h, EPI_RAW, s); }
+    if (head) {
+        GemmArgs h{};
+        h.A = j->xn; h.W = c->head_w; h.M = M; h.N = V; h.K = d; h.out32 = j->logits; h.ldo = V;
+        Timed t(c, "gemm_head");
+        launch_gemm(h, EPI_RAW, s);
+    }
     return CZIP_OK;
 }
 
@@ -599,7 +607,7 @@ extern "C" czip_status czip_compress_plan(czip_ctx* c, const uint32_t* tokens, i
     j->nchunks = (n + chunk - 1) / chunk;
     j->slot = czip_chunk_slot_bytes(chunk);
     const int64_t nch = std::max<int64_t>(j->nchunks, 1);
-    j->BC = pick_batch_chunks(c, nch, chunk);
+    j->BC = pick_batch_chunks(c, nch, chunk, !c->head_fused);
     if ((rc = dalloc(c, j->allocs, &j->tok, (size_t)std::max<int64_t>(n, 1)))) { free_job_mem(j.get()); return rc; }
     if ((rc = dalloc(c, j->allocs, &j->out, (size_t)(nch * j->slot)))) { free_job_mem(j.get()); return rc; }
     if ((rc = dalloc(c, j->allocs, &j->out_lens, (size_t)nch))) { free_job_mem(j.get()); return rc; }
@@ -607,7 +615,7 @@ extern "C" czip_status czip_compress_plan(czip_ctx* c, const uint32_t* tokens, i
     // coder intervals and lengths of every chunk, so one encoder launch covers all chunks
     if ((rc = dalloc(c, j->allocs, &j->lohi_all, (size_t)(nch * chunk * 2)))) { free_job_mem(j.get()); return rc; }
     if ((rc = dalloc(c, j->allocs, &j->lens_all, (size_t)nch))) { free_job_mem(j.get()); return rc; }
-    if ((rc = alloc_scratch(c, j.get(), j->BC, chunk))) { free_job_mem(j.get()); return rc; }
+    if ((rc = alloc_scratch(c, j.get(), j->BC, chunk, !c->head_fused))) { free_job_mem(j.get()); return rc; }
     if (n > 0) {
         hipError_t e = hipMemcpy(j->tok, tokens, (size_t)n * 4, hipMemcpyHostToDevice);
         if (e != hipSuccess) { free_job_mem(j.get()); return fail(c, CZIP_E_HIP, hipGetErrorString(e)); }
@@ -628,9 +636,19 @@ static czip_status run_compress(czip_job* j) {
         const int M = nb * T;
         j->lens = j->lens_all + c0;
         { Timed t(c, "prep"); launch_prep_chunks(j->tok, j->n_tokens, c0, nb, T, j->inp, j->tgt, j->lens, s); }
-        czip_status rc = forward_batch(c, j, nb, T);
+        czip_status rc = forward_batch(c, j, nb, T, !c->head_fused);
         if (rc) return rc;
-        { Timed t(c, "cdf"); launch_cdf(j->logits, M, V, j->tgt, j->lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 0, j->lohi_all, c0 * T, s); }
+        if (c->head_fused) {
+            HeadCdfArgs h{};
+            h.A = j->xn; h.W = c->head_w; h.M = M; h.K = c->cfg.d_model; h.V = V; h.targets = j->tgt; h.lens = j->lens;
+            h.T = T; h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total;
+            h.out = j->lohi_all; h.out_row0 = c0 * T;
+            Timed t(c, "head_cdf");
+            launch_head_cdf(h, s);
+        } else {
+            Timed t(c, "cdf");
+            launch_cdf(j->logits, M, V, j->tgt, j->lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 0, j->lohi_all, c0 * T, s);
+        }
     }
     if (j->nchunks > 0) {
         Timed t(c, "encode");

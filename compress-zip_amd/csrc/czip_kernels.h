@@ -71,6 +71,23 @@ struct RowGemmArgs {
 bool gemm_rn_supported(int d);
 void launch_gemm_rn(const RowGemmArgs& a, hipStream_t s);
 
+// LM head + logits -> (cum_lo, cum_hi) of each row's target (k_cdf mode 0)
+// without the int32 logits leaving the chip; V in {512, 1024}.
+struct HeadCdfArgs {
+    const int8_t* A;           // [M, K] final-normalized rows
+    const int8_t* W;           // [V, K] head weights
+    int M, K, V;
+    const uint32_t* targets;   // [M]
+    const int32_t* lens;       // [M / T]
+    int T;
+    const uint16_t* lut;       // [256]
+    unsigned coef, total;
+    uint32_t* out;             // [., 2]
+    long long out_row0;
+};
+bool head_cdf_supported(int V);
+void launch_head_cdf(const HeadCdfArgs& a, hipStream_t s);
+
 void launch_prep_chunks(const uint32_t* toks, int64_t n_tokens, int64_t chunk0, int nb, int T,
                         uint32_t* inp, uint32_t* tgt, int32_t* lens, hipStream_t s);
 // x may be nullptr (the residual stream is re-read from the embedding rows)

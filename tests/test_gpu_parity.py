@@ -167,13 +167,15 @@ def test_attention_general_path(amd, orc, tmp_path):
 
 def test_unfused_norm_path(amd, orc, tmp_path, monkeypatch):
     """The residual + RMSNorm row kernels that back the row GEMM where it has no
-    instance (three heads) or is switched off, in both passes."""
+    instance (three heads) or is switched off, in both passes; and the separate
+    LM head + interval kernels behind the fused head of compression."""
     from czip_amd import synth
     path = synth.write_random_model(str(tmp_path / "h3.czm"), d=192, n_layers=2, n_heads=3, n_kv=1, d_ff=256,
                                     vocab=1024, ctx=128, seed=90)
     gm, om = _model_pair(amd, orc, path, amd.KV_GQA)
     _check_logits(gm, om, 128, [128, 60], 91, 1024)
     monkeypatch.setenv("CZIP_UNFUSED_NORM", "1")
+    monkeypatch.setenv("CZIP_UNFUSED_HEAD", "1")
     gm2 = amd.Model(amd.ModelWeights(MODEL_PATH))
     lens = [64, 40]
     toks = synth.zipf_ids(sum(lens), 1024, seed=92)
