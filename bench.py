@@ -24,6 +24,13 @@ import numpy as np  # noqa: E402
 PEAK_INT8_TOPS = 5000.0     # TOP/s
 PEAK_HBM_GBS = 8000.0       # GB/s
 
+# HBM bytes per token (read + write) of each kernel on the text workload, from
+# two rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0: the factors a
+# plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text_1Mtok.md
+TRAFFIC_B_PER_TOKEN = {"attention": 994 + 396, "gemm_qkv": 1543 + 606, "gemm_o_norm": 401 + 1152,
+                       "gemm_down_norm": 1833 + 384, "gemm_up": 3072 + 1024, "head_cdf": 391 + 8}
+TRAFFIC_WORKLOADS = ("v001_L4_ctx512_text64MiB",)
+
 WORKLOADS = {
     # shipped model, level 4 (512-token chunks), 64 MiB of seeded synthetic text
     "v001_L4_ctx512_text64MiB": dict(model="shipped", chunk=512, text_bytes=64 << 20),
@@ -170,6 +177,11 @@ def main():
         ach = per_launch / (kernels[dom]["avg_ms"] / 1000.0) / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "kernel": dom}
+
+    if args.workload in TRAFFIC_WORKLOADS and roof["kernel"] in TRAFFIC_B_PER_TOKEN:
+        per_launch_tokens = n / (kernels[dom]["launches"] / args.steps)
+        roof["traffic"] = round(TRAFFIC_B_PER_TOKEN[roof["kernel"]] * per_launch_tokens)
+        roof["traffic_source"] = "rocprofv3 FETCH_SIZE/WRITE_SIZE per token x tokens per launch"
 
     # decompress leg: the chunks just coded, decoded back on the device as
     # concurrent streams (one token per stream per step), checked for identity
