@@ -99,7 +99,14 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int row = lane & 15, grp = lane >> 4;
-    const int q0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
+    // 1-D grid, XCD-aware: workgroups go round-robin over the 8 XCDs; XCD x
+    // takes chunks x, x + 8, ..., all (query block, head) pairs of a chunk in a
+    // row, so a chunk's K/V tiles are fetched into one L2 only.
+    const int nq = (a.T + 63) / 64, per_chunk = nq * a.H;
+    const int xcd = (int)(blockIdx.x % 8u), jx = (int)(blockIdx.x / 8u);
+    const int b = (jx / per_chunk) * 8 + xcd;
+    if (b >= a.B) return;
+    const int q0 = ((jx % per_chunk) % nq) * 64, h = (jx % per_chunk) / nq;
     const int T = a.T, len = a.lens[b];
     if (q0 >= len) return;
     lut32[tid] = (unsigned)a.lut[tid] << 16;
@@ -341,11 +348,13 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
 }
 
 void launch_attention(const AttnArgs& a, int B, hipStream_t s) {
-    dim3 grid((unsigned)((a.T + 63) / 64), (unsigned)a.H, (unsigned)B);
+    AttnArgs g = a;
+    g.B = B;
+    dim3 grid((unsigned)(((B + 7) / 8) * 8 * ((a.T + 63) / 64) * a.H));
     if (a.general)
-        hipLaunchKernelGGL(k_attention<true>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_attention<true>, grid, dim3(256), 0, s, g);
     else
-        hipLaunchKernelGGL(k_attention<false>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_attention<false>, grid, dim3(256), 0, s, g);
 }
 
 }  // namespace czip

@@ -16,6 +16,7 @@ namespace czip {
 // tile, and the epilogues store 4 outputs with one vector store.
 // ---------------------------------------------------------------------------
 constexpr int BM = 128, BN = 128, BK = 64, LDSK = BK + 16;
+constexpr int NXCD = 8;  // XCDs of an MI355X
 
 struct TileRegs {
     int4 v[2];
@@ -68,9 +69,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
-    // N tiles vary fastest so consecutive workgroups reuse the same A rows from L2
+    // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+    // L2: XCD x takes the A blocks m = x, x + 8, ..., all N tiles of one A block
+    // back to back, so every A block is fetched from HBM by one L2 only.
     const int ntn = (a.N + BN - 1) / BN;
-    const int m0 = (int)(blockIdx.x / ntn) * BM, n0 = (int)(blockIdx.x % ntn) * BN;
+    const int xcd = (int)(blockIdx.x % NXCD), jx = (int)(blockIdx.x / NXCD);
+    const int mt = (jx / ntn) * NXCD + xcd;
+    const int m0 = mt * BM, n0 = (jx % ntn) * BN;
+    if (m0 >= a.M) return;
     const int nk = a.K / BK;
 
     v4i acc[4][4];
@@ -204,7 +210,8 @@ static void launch_epi(const GemmArgs& a, dim3 grid, hipStream_t s) {
 }
 
 void launch_gemm(const GemmArgs& a, int epi, hipStream_t s) {
-    dim3 grid((unsigned)(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN)));
+    const int ntm = (a.M + BM - 1) / BM, ntn = (a.N + BN - 1) / BN;
+    dim3 grid((unsigned)(((ntm + NXCD - 1) / NXCD) * NXCD * ntn));
     switch (epi) {
         case EPI_RAW: launch_epi<EPI_RAW>(a, grid, s); break;
         case EPI_REQ: launch_epi<EPI_REQ>(a, grid, s); break;

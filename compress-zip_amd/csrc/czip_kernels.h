@@ -47,6 +47,7 @@ struct AttnArgs {
     int M, T, H, G, KH, kv_mode;
     unsigned coef;
     int general;              // 1: scores may reach 2^30 or lut[0] != 65535 (wrapping score differences)
+    int B;                    // chunks of the launch (set by launch_attention)
 };
 
 // GEMM over full rows (N = d) with the residual + RMSNorm epilogue
