@@ -115,6 +115,29 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     const int col_base = n0 + wn * 64;  // 64-aligned, one head / one gate-up group
     if (col_base >= a.N) return;
     const int c4 = (lane >> 4) * 4;  // first of this lane's 4 consecutive columns in a 16-wide tile
+    // QKV: position and chunk of the lane's 4 rows, and their RoPE cos/sin for
+    // columns i0 .. i0+3 (8-byte loads, all issued before the arithmetic)
+    int rowpos[4], rowchunk[4];
+    unsigned cs[4][2][2], sn2[4][2][2];
+    if (EPI == EPI_QKV) {
+        const float invT = 1.0f / (float)a.T;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = min(m0 + wm * 64 + i * 16 + lr, a.M - 1);
+            int b = (int)((float)row * invT);  // row < 2^24: within one of row / T
+            if (b * a.T > row) b--;
+            else if ((b + 1) * a.T <= row) b++;
+            rowpos[i] = a.pos >= 0 ? a.pos : row - b * a.T;
+            rowchunk[i] = a.pos >= 0 ? row : b;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint2 c = *(const uint2*)(a.rcos + rowpos[i] * 32 + j * 16 + c4);
+                const uint2 sv = *(const uint2*)(a.rsin + rowpos[i] * 32 + j * 16 + c4);
+                cs[i][j][0] = c.x; cs[i][j][1] = c.y;
+                sn2[i][j][0] = sv.x; sn2[i][j][1] = sv.y;
+            }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int row = m0 + wm * 64 + i * 16 + lr;
@@ -146,7 +169,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
                 *(unsigned*)(a.out8 + (size_t)row * a.ldo + (col_base >> 1) + j * 16 + c4) = pack4i(o[0], o[1], o[2], o[3]);
             }
         } else {  // EPI_QKV
-            const int p = a.pos >= 0 ? a.pos : row % a.T, b = a.pos >= 0 ? row : row / a.T;
+            const int p = rowpos[i], b = rowchunk[i];
             const int kcol = col_base - a.d;
             int g = 0, isv = 0;
             if (kcol >= 0) {
@@ -161,9 +184,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
                 for (int r = 0; r < 4; r++) {
                     xv[r] = rq<FAST>(acc[i][j][r], a);
                     yv[r] = rq<FAST>(acc[i][j + 2][r], a);
-                    const int c = a.rcos[p * 32 + i0 + r], s = a.rsin[p * 32 + i0 + r];
-                    const int xr = (int)((unsigned)(xv[r] * c) - (unsigned)(yv[r] * s));
-                    const int yr = (int)((unsigned)(xv[r] * s) + (unsigned)(yv[r] * c));
+                    const int c = (int16_t)(r & 1 ? cs[i][j][r >> 1] >> 16 : cs[i][j][r >> 1] & 0xFFFFu);
+                    const int sn = (int16_t)(r & 1 ? sn2[i][j][r >> 1] >> 16 : sn2[i][j][r >> 1] & 0xFFFFu);
+                    const int xr = (int)((unsigned)(xv[r] * c) - (unsigned)(yv[r] * sn));
+                    const int yr = (int)((unsigned)(xv[r] * sn) + (unsigned)(yv[r] * c));
                     if (kcol < 0) {
                         // Q: attention.rs:53-83 (>>15 then NET_SHIFT=1, two roundings)
                         xq[r] = clamp127(rne_shr(rne_shr(xr, 15), 1));
