@@ -321,6 +321,28 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
     }
 
     // epilogue.  Lane holds columns nb + 16 t + c4 .. +3 of rows m0 + 16 i + lr.
+    // Its global operands (norm weights of its columns, residual input of its
+    // rows: int16 stream or the token's embedding row) are all requested first
+    // so that their latency hides behind steps 1 and the first reduction.
+    unsigned w1r[CT], w2r[CT];
+    uint2 xr[4][CT];
+#pragma unroll
+    for (int t = 0; t < CT; t++) {
+        w1r[t] = *(const unsigned*)(a.w1 + nb + t * 16 + c4);
+        w2r[t] = *(const unsigned*)(a.w2 + nb + t * 16 + c4);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = min(m0 + i * 16 + lr, a.M - 1);
+        if (a.x_in) {
+#pragma unroll
+            for (int t = 0; t < CT; t++) xr[i][t] = *(const uint2*)(a.x_in + (size_t)row * a.d + nb + t * 16 + c4);
+        } else {
+            const int8_t* erow = a.embed + (size_t)a.tok[row] * a.d;
+#pragma unroll
+            for (int t = 0; t < CT; t++) xr[i][t] = make_uint2(*(const unsigned*)(erow + nb + t * 16 + c4), 0u);
+        }
+    }
     // 1. y = requant(acc); row sums of y^2
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -355,22 +377,17 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
         const int row = m0 + i * 16 + lr;
         const bool live = row < a.M;
         const int inv = inv_s[i * 16 + lr];
-        const int8_t* erow = nullptr;
-        if (!a.x_in && live) erow = a.embed + (size_t)a.tok[row] * a.d;
         unsigned ss = 0;
 #pragma unroll
         for (int t = 0; t < CT; t++) {
             const int n = nb + t * 16 + c4;
-            int w1v[4], xo[4] = {0, 0, 0, 0};
-            unpack4s(*(const unsigned*)(a.w1 + n), w1v);
-            if (live) {
-                if (a.x_in) {
-                    const uint2 xv = *(const uint2*)(a.x_in + (size_t)row * a.d + n);
-                    xo[0] = (int16_t)(xv.x & 0xFFFFu); xo[1] = (int16_t)(xv.x >> 16);
-                    xo[2] = (int16_t)(xv.y & 0xFFFFu); xo[3] = (int16_t)(xv.y >> 16);
-                } else {
-                    unpack4s(*(const unsigned*)(erow + n), xo);
-                }
+            int w1v[4], xo[4];
+            unpack4s(w1r[t], w1v);
+            if (a.x_in) {
+                xo[0] = (int16_t)(xr[i][t].x & 0xFFFFu); xo[1] = (int16_t)(xr[i][t].x >> 16);
+                xo[2] = (int16_t)(xr[i][t].y & 0xFFFFu); xo[3] = (int16_t)(xr[i][t].y >> 16);
+            } else {
+                unpack4s(xr[i][t].x, xo);
             }
             int xnw[4];
 #pragma unroll
@@ -400,7 +417,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
         for (int t = 0; t < CT; t++) {
             const int n = nb + t * 16 + c4;
             int w2v[4];
-            unpack4s(*(const unsigned*)(a.w2 + n), w2v);
+            unpack4s(w2r[t], w2v);
             *(unsigned*)(a.xn + (size_t)row * a.d + n) =
                 pack4i(rms_el(acc[i][t][0], w2v[0], inv), rms_el(acc[i][t][1], w2v[1], inv),
                        rms_el(acc[i][t][2], w2v[2], inv), rms_el(acc[i][t][3], w2v[3], inv));

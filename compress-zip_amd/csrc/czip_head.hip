@@ -80,6 +80,10 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
         __syncthreads();
     }
 
+    // targets of the lane's rows, requested before the reductions
+    int tokr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) tokr[i] = m0 + i * 16 + lr < a.M ? (int)a.targets[m0 + i * 16 + lr] : 0;
     // 1. row max
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -150,7 +154,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
         const int rr = i * 16 + lr;
         const unsigned S = row_S[rr], Q = row_Q[rr], Rm = row_Rm[rr];
         const float rf = row_rf[rr];
-        const int tok = m0 + rr < a.M ? (int)a.targets[m0 + rr] : 0;
+        const int tok = tokr[i];
         unsigned fs = 0, lo = 0, ft = 0;
 #pragma unroll
         for (int t = 0; t < CT; t++)
