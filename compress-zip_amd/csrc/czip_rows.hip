@@ -67,9 +67,8 @@ __device__ __forceinline__ void rms_row(const RowI8& x, const int8_t* __restrict
 #pragma unroll
             for (int k = 0; k < 4; k++) ss += (unsigned)(x.v[j][k] * x.v[j][k]);
     ss = wave_sum_u(ss);
-    int mean_sq = (int)(ss / (unsigned)d) + 1;  // eps_scaled = 1 (rmsnorm.rs:80-83)
-    if (mean_sq < 1) mean_sq = 1;
-    const int inv = inv_rms_q15(mean_sq);
+    const int mean_sq = (int)(ss / (unsigned)d) + 1;  // eps_scaled = 1 (rmsnorm.rs:80-83); <= 127^2 + 1
+    const int inv = inv_rms_q15_fast(mean_sq);
 #pragma unroll
     for (int j = 0; j < RG; j++) {
         const int g = lane + 64 * j;

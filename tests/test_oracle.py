@@ -182,6 +182,38 @@ def test_inv_rms_exhaustive(orc):
         assert L.orc_inv_rms_q15(ms) == exp
 
 
+def test_inv_rms_f64_form_exhaustive(orc):
+    """The device's inv_rms form (f64 sqrt + exact integer correction, f64
+    quotient estimate + exact remainder test) against the oracle on every
+    mean_sq < 2^16.  The corrections tolerate a +-1 error of either f64
+    estimate, so this pins the algorithm whatever the hardware rounding."""
+    L = orc.lib()
+
+    def fast(ms, sq_err=0, q_err=0):
+        x = max(ms, 1) << 16
+        r = int(math.sqrt(float(x))) + sq_err
+        if r * r > x:
+            r -= 1
+        if (r + 1) * (r + 1) <= x:
+            r += 1
+        q = int(8388608.0 / float(r)) + q_err
+        rem = 8388608 - q * r
+        if rem < 0:
+            q, rem = q - 1, rem + r
+        if rem >= r:
+            q, rem = q + 1, rem - r
+        tr = 2 * rem
+        inv = q + 1 if tr > r else (q + (q & 1) if tr == r else q)
+        return min(max(inv, 1), 32768)
+
+    for ms in range(0, 1 << 16):
+        exp = L.orc_inv_rms_q15(ms)
+        assert fast(ms) == exp, ms
+        if ms % 97 == 0:
+            for e1 in (-1, 1):
+                assert fast(ms, sq_err=e1) == exp and fast(ms, q_err=e1) == exp, ms
+
+
 def test_reglu_exhaustive(orc):
     L = orc.lib()
     g = np.repeat(np.arange(-127, 128), 255).astype(np.int8)
