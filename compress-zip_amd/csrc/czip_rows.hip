@@ -84,41 +84,62 @@ __device__ __forceinline__ void rms_row(const RowI8& x, const int8_t* __restrict
     }
 }
 
-// x = E[tok] (model.rs:372-374); xn = rmsnorm(clamp(x), w) (model.rs:384-385)
+// x = E[tok] (model.rs:372-374); xn = rmsnorm(clamp(x), w) (model.rs:384-385).
+// Sixteen lanes per row, four rows per wavefront: lane s of a row owns the
+// 4-element groups g = s, s + 16, ... (d <= 1024: at most 16 groups), so the
+// four rows' gather -> reduce -> normalize chains overlap.
 __global__ __launch_bounds__(256) void k_embed_norm(const uint32_t* __restrict__ inp, const int8_t* __restrict__ embed,
                                                     const int8_t* __restrict__ w, int M, int d,
                                                     int16_t* __restrict__ x, int8_t* __restrict__ xn) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= M) return;
+    constexpr int G16 = 16;  // groups per lane: d <= 16 * 4 * 16
+    const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int sl = threadIdx.x & 15;
+    const bool live = row < M;
     const int ng = d >> 2;
-    const int8_t* e = embed + (size_t)inp[row] * d;
-    RowI8 xi, y;
+    const int8_t* e = embed + (size_t)(live ? inp[row] : 0u) * d;
+    unsigned raw[G16];
 #pragma unroll
-    for (int j = 0; j < RG; j++) {
-        const int g = lane + 64 * j;
+    for (int j = 0; j < G16; j++) {
+        const int g = sl + 16 * j;
+        raw[j] = g < ng ? *(const unsigned*)(e + 4 * g) : 0u;
+    }
+    unsigned ss = 0;
+#pragma unroll
+    for (int j = 0; j < G16; j++) {
+        int v[4];
+        unpack4(raw[j], v);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int c = clamp127(v[k]);
+            ss += (unsigned)(c * c);
+        }
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) ss += (unsigned)__shfl_xor((int)ss, o, 64);
+    const int inv = inv_rms_q15_fast((int)(ss / (unsigned)d) + 1);  // eps_scaled = 1 (rmsnorm.rs:80-83)
+    if (!live) return;
+#pragma unroll
+    for (int j = 0; j < G16; j++) {
+        const int g = sl + 16 * j;
         if (g < ng) {
-            unpack4(*(const unsigned*)(e + 4 * g), xi.v[j]);
+            int v[4], wv[4], y[4];
+            unpack4(raw[j], v);
+            unpack4(*(const unsigned*)(w + 4 * g), wv);
             if (x) {
-                const unsigned lo = ((unsigned)xi.v[j][0] & 0xFFFFu) | ((unsigned)xi.v[j][1] << 16);
-                const unsigned hi = ((unsigned)xi.v[j][2] & 0xFFFFu) | ((unsigned)xi.v[j][3] << 16);
+                const unsigned lo = ((unsigned)v[0] & 0xFFFFu) | ((unsigned)v[1] << 16);
+                const unsigned hi = ((unsigned)v[2] & 0xFFFFu) | ((unsigned)v[3] << 16);
                 *(uint2*)(x + (size_t)row * d + 4 * g) = make_uint2(lo, hi);
             }
 #pragma unroll
-            for (int k = 0; k < 4; k++) xi.v[j][k] = clamp127(xi.v[j][k]);
+            for (int k = 0; k < 4; k++) y[k] = clamp127(rne_shr(clamp127(v[k]) * wv[k] * inv, 15));
+            *(unsigned*)(xn + (size_t)row * d + 4 * g) = pack4(y);
         }
-    }
-    rms_row(xi, w, d, lane, y);
-#pragma unroll
-    for (int j = 0; j < RG; j++) {
-        const int g = lane + 64 * j;
-        if (g < ng) *(unsigned*)(xn + (size_t)row * d + 4 * g) = pack4(y.v[j]);
     }
 }
 
 void launch_embed_norm(const uint32_t* inp, const int8_t* embed, const int8_t* w, int M, int d, int16_t* x,
                        int8_t* xn, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed_norm, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, s, inp, embed, w, M, d, x, xn);
+    hipLaunchKernelGGL(k_embed_norm, dim3((unsigned)((M + 15) / 16)), dim3(256), 0, s, inp, embed, w, M, d, x, xn);
 }
 
 // x += rmsnorm(y8, w1) (model.rs:429-434 / 463-468);
