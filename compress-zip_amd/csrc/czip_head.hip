@@ -14,7 +14,8 @@ namespace czip {
 //   1. max logit;
 //   2. first argmax, S = sum E(l - max);
 //   3. sum f, f below the target and f of the target, with
-//      f = 1 + e*Q + floor(e*Rm / S) (Q = R / S, Rm = R % S, R = total - V).
+//      f = 1 + e*Q + floor(e*Rm / S) (Q = R / S, Rm = R % S, R = total - V),
+//      the small floor quotient exact in f64.
 // Lane l holds logits of rows 16 i + l % 16 (i < 4) at columns
 // 16 t + 4 (l / 16) .. +3 of its wave's range (t < CT).
 // ---------------------------------------------------------------------------
@@ -27,8 +28,8 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
     __shared__ int red_a[HNW][HBM_ROWS];
     __shared__ unsigned red_b[HNW][HBM_ROWS], red_c[HNW][HBM_ROWS];
     __shared__ int row_i[HBM_ROWS], row_am[HBM_ROWS];
-    __shared__ unsigned row_S[HBM_ROWS], row_Q[HBM_ROWS], row_Rm[HBM_ROWS];
-    __shared__ float row_rf[HBM_ROWS];
+    __shared__ unsigned row_Q[HBM_ROWS];
+    __shared__ double row_Rm[HBM_ROWS], row_inv[HBM_ROWS];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int m0 = blockIdx.x * HBM_ROWS;
@@ -139,21 +140,23 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
             am = min(am, red_a[w][lane]);
             S += red_b[w][lane];
         }
-        const unsigned R = a.total - (unsigned)a.V;  // S <= 8192 * 65535 < 2^32
+        const unsigned R = a.total - (unsigned)a.V;  // S <= 1024 * 65535 < 2^26
         const unsigned Q = R / S;
         row_am[lane] = am;
-        row_S[lane] = S;
         row_Q[lane] = Q;
-        row_Rm[lane] = R - Q * S;
-        row_rf[lane] = (float)(R - Q * S) / (float)S;
+        row_Rm[lane] = (double)(R - Q * S);
+        row_inv[lane] = 1.0 / (double)S;
     }
     __syncthreads();
-    // 3. f = 1 + e*Q + floor(e*Rm/S); sum f, f below the target, f of the target
+    // 3. f = 1 + e*Q + floor(e*Rm/S); sum f, f below the target, f of the target.
+    // floor(e*Rm/S) = floor(fma(e*Rm, 1/S, 2^-30)) in f64: e*Rm < 2^42 is exact,
+    // a nonzero fraction of e*Rm/S is >= 1/S >= 2^-26, and the f64 error of the
+    // product with the rounded 1/S is < 2^-35 for quotients below 2^16.
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int rr = i * 16 + lr;
-        const unsigned S = row_S[rr], Q = row_Q[rr], Rm = row_Rm[rr];
-        const float rf = row_rf[rr];
+        const unsigned Q = row_Q[rr];
+        const double Rm = row_Rm[rr], inv = row_inv[rr];
         const int tok = tokr[i];
         unsigned fs = 0, lo = 0, ft = 0;
 #pragma unroll
@@ -162,10 +165,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
             for (int r = 0; r < 4; r++) {
                 const int col = nb + t * 16 + c4 + r;
                 const unsigned e = (unsigned)acc[i][t][r];
-                unsigned q = (unsigned)((float)e * rf);
-                const unsigned long long tt = (unsigned long long)e * Rm, u = (unsigned long long)q * S;
-                if (tt < u) q -= 1;
-                else if (tt - u >= S) q += 1;
+                const unsigned q = (unsigned)__builtin_fma((double)e * Rm, inv, 0x1p-30);
                 const unsigned f = 1u + e * Q + q;
                 fs += f;
                 lo += col < tok ? f : 0u;
