@@ -103,6 +103,19 @@ __device__ __forceinline__ unsigned exp_q16(int diff, const uint16_t* lut, unsig
     return out < 1u ? 1u : (out > 65535u ? 65535u : out);
 }
 
+// exp_q16 (lut.rs:213-235 / softmax_cdf.rs:55-77) without branches, from a
+// table pre-shifted by 16 bits (lut32[i] = lut[i] << 16): for ip <= 16,
+// (65536 >> ip) * lut == (lut << 16) >> ip; for 17 <= ip <= 31 both round to 0
+// and clamp to 1; ip is capped at 31 like the early return.
+__device__ __forceinline__ unsigned exp_q16_bf(int diff, const unsigned* lut32, unsigned coef) {
+    const unsigned neg = 0u - (unsigned)diff;
+    const unsigned long long pr = (unsigned long long)neg * coef + (1ull << 23);
+    const unsigned t = (unsigned)(pr >> 24);
+    const unsigned ip = min(t >> 8, 31u);
+    const unsigned x = max(((lut32[t & 255u] >> ip) + 0x8000u) >> 16, 1u);
+    return diff >= 0 ? 65535u : x;
+}
+
 // primitives.rs:163-185 (the result is formed with i32 wrap like `as i32 * sign`)
 __device__ __forceinline__ int div_rne_s32_u64(int num, unsigned long long den) {
     if (den == 0) return 0;

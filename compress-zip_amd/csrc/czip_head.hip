@@ -24,7 +24,7 @@ constexpr int HBM_ROWS = 64, HBK = 64, HLDSK = HBK + 16, HNW = 16;
 template <int CT>
 __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
     __shared__ __attribute__((aligned(16))) int8_t As[2][HBM_ROWS * HLDSK];
-    __shared__ uint16_t lut[256];
+    __shared__ unsigned lut32[256];
     __shared__ int red_a[HNW][HBM_ROWS];
     __shared__ unsigned red_b[HNW][HBM_ROWS], red_c[HNW][HBM_ROWS];
     __shared__ int row_i[HBM_ROWS], row_am[HBM_ROWS];
@@ -36,7 +36,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
     const int nb = wave * CT * 16;
     const int lr = lane & 15, lk = (lane >> 4) * 16, c4 = (lane >> 4) * 4;
     const int nk = a.K / HBK;
-    if (tid < 256) lut[tid] = a.lut[tid];
+    if (tid < 256) lut32[tid] = (unsigned)a.lut[tid] << 16;
 
     v4i acc[4][CT];
 #pragma unroll
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
                 const int col = nb + t * 16 + c4 + r;
                 const int l = acc[i][t][r];
                 am = (l == mx && col < am) ? col : am;
-                const unsigned e = exp_q16((int)((unsigned)l - (unsigned)mx), lut, a.coef);
+                const unsigned e = exp_q16_bf((int)((unsigned)l - (unsigned)mx), lut32, a.coef);
                 acc[i][t][r] = (int)e;
                 s += e;
             }
