@@ -301,11 +301,11 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
             int sw = sh * 256 + sl;  // sum over this lane's 16 keys of (w_j - 32896)
             sw += __shfl_xor(sw, 16, 64);
             sw += __shfl_xor(sw, 32, 64);
+            // rescale factor of this lane's row at record j (0: none); row r's is
+            // read by the combine from lane r
+            const unsigned erow = (j >= 1 && j <= nrow) ? (unsigned)W.rec_e[row][j - 1] : 0u;
             // 4a. S of this lane's row (lanes = rows): rescale at record j, then add segment j
-            if (j >= 1 && j <= nrow) {
-                const unsigned e = W.rec_e[row][j - 1];
-                if (e) S = rescale_s64(S, e);
-            }
+            if (erow) S = rescale_s64(S, erow);
             S += (unsigned)sw + 64u * WOFF;
 #pragma unroll
             for (int db = 0; db < 4; db++) {
@@ -322,10 +322,8 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 if (j <= nr[r]) {
-                    if (j >= 1) {
-                        const unsigned e = (unsigned)__builtin_amdgcn_readfirstlane(W.rec_e[r][j - 1]);
-                        if (e) vacc[r] = rescale_v(vacc[r], e);
-                    }
+                    const unsigned e = (unsigned)__builtin_amdgcn_readlane((int)erow, r);
+                    if (e) vacc[r] = rescale_v(vacc[r], e);
                     vacc[r] += bv[r] + corr;
                 }
             }
