@@ -723,7 +723,7 @@ extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t* data, co
     const size_t d = (size_t)c->cfg.d_model, L = (size_t)c->cfg.n_layers;
     double gb = 16.0;
     if (const char* s = getenv("CZIP_SCRATCH_GB")) gb = atof(s);
-    const double per_stream = (double)row_bytes(c) + 2.0 * L * (double)c->KH * Tcap * 64 + 64;
+    const double per_stream = (double)row_bytes(c) + 2.0 * L * (double)c->KH * pad64(Tcap) * 64 + 64;
     int64_t S = (int64_t)(gb * 1e9 / per_stream);
     if (const char* s = getenv("CZIP_DECODE_STREAMS")) S = std::min<int64_t>(S, atoll(s));
     S = std::max<int64_t>(1, std::min<int64_t>(S, std::max(nchunks, 1)));
@@ -744,8 +744,8 @@ extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t* data, co
         (rc = dalloc(c, A, &j->q8, (size_t)S * d)) || (rc = dalloc(c, A, &j->attn, (size_t)S * d)) ||
         (rc = dalloc(c, A, &j->y8, (size_t)S * d)) || (rc = dalloc(c, A, &j->r8, (size_t)S * c->cfg.d_ff)) ||
         (rc = dalloc(c, A, &j->logits, (size_t)S * c->cfg.vocab)) ||
-        (rc = dalloc(c, A, &j->kc, L * (size_t)S * c->KH * Tcap * 64)) ||
-        (rc = dalloc(c, A, &j->vc, L * (size_t)S * c->KH * Tcap * 64))) {
+        (rc = dalloc(c, A, &j->kc, L * (size_t)S * c->KH * pad64(Tcap) * 64)) ||
+        (rc = dalloc(c, A, &j->vc, L * (size_t)S * c->KH * pad64(Tcap) * 64))) {
         free_job_mem(j.get());
         return rc;
     }
@@ -768,7 +768,10 @@ static czip_status run_decompress(czip_job* j) {
     hipStream_t s = c->stream;
     const int d = c->cfg.d_model, F = c->cfg.d_ff, V = c->cfg.vocab, H = c->cfg.n_heads;
     const int Tc = j->T;
-    const size_t layer_kv = (size_t)j->S * c->KH * Tc * 64;
+    // KV caches per layer: K and V [S][KH][TP][64] (key-major); TP = the
+    // longest stream rounded up to whole 64-key tiles
+    const int TP = pad64(Tc);
+    const size_t layer_kv = (size_t)j->S * c->KH * TP * 64;
     for (int64_t g0 = 0; g0 < j->nchunks; g0 += j->S) {
         const int S = (int)std::min<int64_t>(j->S, j->nchunks - g0);
         int steps = 0;
@@ -786,12 +789,12 @@ static czip_status run_decompress(czip_job* j) {
                 GemmArgs g{};
                 g.A = j->xn; g.W = L.qkv_w; g.M = S; g.N = L.qkv_n; g.K = d;
                 g.out8 = j->q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
-                g.d = d; g.T = Tc; g.TP = Tc; g.pos = p; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
+                g.d = d; g.T = TP; g.TP = TP; g.pos = p; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
                 g.KH = c->KH; g.kc = kc; g.vc = vc; g.rcos = c->rcos; g.rsin = c->rsin;
                 { Timed t(c, "gemm_qkv"); launch_gemm(g, EPI_QKV, s); }
                 AttnArgs a{};
-                a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = Tc; a.lens = j->d_ntok + g0; a.score_mult = L.score_mult;
-                a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = S; a.T = Tc; a.H = H; a.G = c->cfg.n_kv_heads;
+                a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = j->d_ntok + g0; a.score_mult = L.score_mult;
+                a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = S; a.T = TP; a.H = H; a.G = c->cfg.n_kv_heads;
                 a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;
                 a.general = L.attn_general;
                 { Timed t(c, "attn_decode"); launch_attn_decode(a, S, p, s); }

@@ -207,7 +207,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
                     *(unsigned*)(k + i0) = pack4i(xq[0], xq[1], xq[2], xq[3]);
                     *(unsigned*)(k + i0 + 32) = pack4i(yq[0], yq[1], yq[2], yq[3]);
                 } else if (a.pos >= 0) {
-                    // V of a decode step: key-major like K
+                    // V of a decode step: key-major like K (one contiguous row per
+                    // stream; the decode attention transposes its tiles in LDS)
                     int8_t* v = a.vc + (((size_t)b * a.KH + g) * a.T + p) * 64;
                     *(unsigned*)(v + i0) = pack4i(xv[0], xv[1], xv[2], xv[3]);
                     *(unsigned*)(v + i0 + 32) = pack4i(yv[0], yv[1], yv[2], yv[3]);
