@@ -125,8 +125,9 @@ def main():
     weights = czip_amd.ModelWeights(model_path, kv_mode)
     cfg = weights.config
     tokens, text, tokenizer = make_tokens(wl, weights, cfg["vocab_size"])
-    if args.tokens:
+    if args.tokens and args.tokens < tokens.size:
         tokens = tokens[:args.tokens]
+        text = None  # a token prefix: the round trip is checked on the ids only
     chunk = wl["chunk"]
     n = int(tokens.size)
     log(f"workload {args.workload}: {n} tokens, chunk {chunk}")

@@ -1,94 +1,15 @@
 // Exact causal attention of the prefill (attention.rs:162-289) on MFMA.
-#include "czip_device.h"
+#include "czip_attn_tile.h"
 #include "czip_kernels.h"
 
 namespace czip {
 
 // ---------------------------------------------------------------------------
-// The reference walks the keys of a query row in order and, each time the
-// running max strictly increases (a "record"), rescales the running sum S and
-// the value accumulator with a rounded factor (attention.rs:205-276).  Between
-// records every weight uses the same max, so a segment's contribution is a
-// plain integer sum (S in u64, vacc modulo 2^32) that can be formed in any
-// order; only the rescales must be applied in key order.
-//
-// One workgroup = one chunk, one head, 64 query rows (4 waves x 16 rows).
-// Per 64-key tile (the next tile's K and V^T are fetched into registers
-// meanwhile) each wave:
-//  1. forms S^T = K Q^T (int8 MFMA) and the score epilogue in f64, which is
-//     exact: |dot / 4 * mult| < 2^49;
-//  2. scans its rows' keys in order (a lane owns 16 consecutive keys of one
-//     row): running max, records, one exp per key.  A key's weight and, at a
-//     record, the rescale factor are both E(-|s - max before the key|);
-//  3. for each segment index j = 0..max records, forms the segment sums of
-//     all 16 rows at once, O_j^T = V^T P_j^T, on int8 MFMA.  The 16-bit
-//     weights enter as two signed bytes: w - 32896 = 256*hi + lo, keys outside
-//     segment j carry w = 0, and the constant 32896 * sum(v) is added back;
-//  4. hands O_j through LDS to a "lanes = head dims" layout and walks each
-//     row's own segments: rescale at the record, then add (rows with fewer
-//     records skip the pass with a scalar branch); S is kept with lanes = rows.
-// Scores are kept as s ^ 2^31 so that unsigned order is signed order; 0 is
-// INT32_MIN, the reference's "nothing seen yet".
+// One workgroup = one chunk, one head, 64 query rows (4 waves x 16 rows).  The
+// K / V^T tiles of 64 keys are staged in LDS once for the 4 waves (the next
+// tile is fetched into registers meanwhile); each wave runs attn_tile over
+// its 16 rows.
 // ---------------------------------------------------------------------------
-
-constexpr int KLD = 80;               // LDS row stride (bytes) of the K tile and of the V^T tile
-constexpr unsigned WOFF = 32896;      // w - WOFF spans [-32896, 32639] = 256*[-128,127] + [-128,127]
-constexpr unsigned BIAS = 0x80000000u;
-constexpr int RS = 68;                // row stride (words) of the per-wave buffer: 16-byte accesses of 16 rows hit 64 banks
-
-struct AttnWaveLds {
-    unsigned buf[16][RS];    // scores [row][key]; then per pass: column sums [column][dim]
-    uint16_t rec_e[16][64];  // rescale factor at record j+1 of row r (0: nothing to rescale)
-    int nrec[16];            // records of each row in the tile
-};
-
-__device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
-
-// sra_rne64(sra_rne32(dot, 2) * mult, 15) (attention.rs:233-239), biased.
-// RNE of a quotient by 2^k is symmetric, so the floor form
-// (x + 2^(k-1) - 1 + bit_k(x)) >> k equals the reference's sign-magnitude one;
-// the product is exact in f64 and rint rounds half to even.
-template <bool GEN>
-__device__ __forceinline__ unsigned score_b(int dot, double mscale) {
-    const int du = (dot + 1 + ((dot >> 2) & 1)) >> 2;
-    double r = __builtin_rint((double)du * mscale);
-    if (GEN) r = fmin(fmax(r, -2147483648.0), 2147483647.0);
-    return (unsigned)(int)r ^ BIAS;
-}
-
-// exp_q16(-neg) (lut.rs:213-235) with the table pre-shifted by 16 bits.
-// (65536 >> ip) * lut == (lut << 16) >> ip for ip <= 16, and both round to 0
-// (then clamp to 1) for ip >= 17; ip is capped at 31 like the reference's
-// early return.  neg == 0 reads lut[0], which the fast path requires to be 65535.
-__device__ __forceinline__ unsigned exp_neg(unsigned neg, const unsigned* lut32) {
-    const unsigned long long pr = (unsigned long long)neg * ATTN_COEF_Q24 + (1ull << 23);
-    const unsigned t = (unsigned)(pr >> 24);
-    const unsigned ip = min(t >> 8, 31u);
-    const unsigned x = ((lut32[t & 255u] >> ip) + 0x8000u) >> 16;
-    return max(x, 1u);
-}
-
-// vacc rescale at a record (attention.rs:246-261): ((i64)v * e +- 2^15) >> 16,
-// formed from 16-bit halves of v with 24-bit multiplies (e in 1..65535).
-__device__ __forceinline__ unsigned rescale_v(unsigned v, unsigned e) {
-    const int vh = (int)v >> 16;
-    const unsigned t = __umul24(v & 0xFFFFu, e);
-    return (unsigned)__mul24(vh, (int)e) + (t >> 16) + ((t >> 15) & 1u) + (unsigned)((int)v >> 31);
-}
-
-// S rescale at a record (attention.rs:246-250): (S * e + 0x8000) >> 16
-__device__ __forceinline__ unsigned long long rescale_s64(unsigned long long S, unsigned e) {
-    return (S * e + 0x8000ull) >> 16;
-}
-
-// bytes of x equal to zero -> 0xFF, others -> 0x00 (exact per byte)
-__device__ __forceinline__ unsigned zero_bytes_mask(unsigned x) {
-    unsigned t = ((x & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | x;
-    t = ~t & 0x80808080u;
-    return (t >> 7) * 0xFFu;
-}
-
-__device__ __forceinline__ unsigned pick(unsigned msk, unsigned a, unsigned b) { return (a & msk) | (b & ~msk); }
 
 template <bool GEN>
 __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
@@ -114,7 +35,7 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     const int D = a.H * 64;
     const int g = a.kv_mode == 1 ? (h * a.G) / a.H : 0;
     const int8_t* Kg = a.kc + ((size_t)b * a.KH + g) * T * 64;
-    const int8_t* Vg = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP;
+    const int8_t* Vg = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP;  // [TP/16][64][16]
     const double mscale = (double)a.score_mult[h] * (1.0 / 32768.0);
     const int p = q0 + wave * 16 + row;  // query position of this lane's row (scan / MFMA layouts)
     const int wrow0 = q0 + wave * 16;
@@ -124,30 +45,27 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     v4i qop = (v4i){0, 0, 0, 0};
     if (p < T) qop = *(const v4i*)(a.q + ((size_t)b * T + p) * D + h * 64 + grp * 16);
 
-    // state: running max m (biased) and weight sum S with lanes = rows
-    // (replicated over the 4 lane groups); vacc with lanes = head dims
-    // (register index = row)
-    unsigned m = 0u;
-    unsigned long long S = 0;
-    unsigned vacc[16];
-    for (int r = 0; r < 16; r++) vacc[r] = 0;
+    AttnRows st;
+    st.m = 0u;
+    st.S = 0;
+    for (int r = 0; r < 16; r++) st.vacc[r] = 0;
     if (a.sink) {  // attention.rs:211-224: sink score is the initial max, weight E(0) = 65535
         const int* sk = (const int*)(a.sink + grp * 16);
         int dot = 0;
         for (int i = 0; i < 4; i++) dot = __builtin_amdgcn_sdot4(qop[i], sk[i], dot, false);
         dot += __shfl_xor(dot, 16, 64);
         dot += __shfl_xor(dot, 32, 64);
-        m = score_b<GEN>(dot, mscale);
-        S = 65535ull;
+        st.m = score_b<GEN>(dot, mscale);
+        st.S = 65535ull;
     }
 
     const int ntiles = (min(q0 + 63, len - 1)) / 64 + 1;
-    // K / V^T tile of 64 keys: thread -> row tid/4, 16 bytes; the next tile is
-    // fetched into registers while the current one is processed
+    // K / V^T tile of 64 keys: thread -> row tid/4, 16 bytes; V^T is stored
+    // in blocks of 16 keys ([key/16][dim][16])
     const int ldr = tid >> 2, ldc = (tid & 3) * 16;
     int4 kreg = make_int4(0, 0, 0, 0), vreg;
     if (ldr < T) kreg = *(const int4*)(Kg + (size_t)ldr * 64 + ldc);
-    vreg = *(const int4*)(Vg + (size_t)ldr * a.TP + ldc);
+    vreg = *(const int4*)(Vg + ((size_t)(ldc >> 4) * 64 + ldr) * 16);
     for (int kt = 0; kt < ntiles; kt++) {
         const int t0 = kt * 64;
         __syncthreads();
@@ -158,189 +76,26 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
             const int t1 = t0 + 64;
             kreg = make_int4(0, 0, 0, 0);
             if (t1 + ldr < T) kreg = *(const int4*)(Kg + (size_t)(t1 + ldr) * 64 + ldc);
-            vreg = *(const int4*)(Vg + (size_t)ldr * a.TP + t1 + ldc);
+            vreg = *(const int4*)(Vg + ((size_t)((t1 + ldc) >> 4) * 64 + ldr) * 16);
         }
         if (!wave_live || t0 > wave_last) continue;
-
-        // 1. S^T = K Q^T, score epilogue, stored [row][key]
-#pragma unroll
-        for (int blk = 0; blk < 4; blk++) {
-            v4i kop = *(const v4i*)(Ks + (blk * 16 + row) * KLD + grp * 16);
-            v4i st = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, qop, (v4i){0, 0, 0, 0}, 0, 0, 0);
-            *(uint4*)&W.buf[row][blk * 16 + grp * 4] = make_uint4(score_b<GEN>(st[0], mscale), score_b<GEN>(st[1], mscale),
-                                                                  score_b<GEN>(st[2], mscale), score_b<GEN>(st[3], mscale));
-        }
-        wave_lds_fence();
-
-        // 2. in-order scan of keys [16*grp, 16*grp+16) of this row
-        unsigned sv[16];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint4 v = *(const uint4*)&W.buf[row][grp * 16 + i * 4];
-            sv[i * 4] = v.x; sv[i * 4 + 1] = v.y; sv[i * 4 + 2] = v.z; sv[i * 4 + 3] = v.w;
-        }
-        const bool diag = t0 + 63 > wrow0;  // some key of the tile is after some row of the wave
         int nvalid = p - (t0 + grp * 16) + 1;  // keys t <= p are visible (causal)
         nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
-        if (diag) {
-#pragma unroll
-            for (int k = 0; k < 16; k++)
-                if (k >= nvalid) sv[k] = 0u;  // INT32_MIN: never a record; weight masked below
-        }
-        unsigned bmax = 0u;
-#pragma unroll
-        for (int k = 0; k < 16; k++) bmax = max(bmax, sv[k]);
-        const unsigned e1 = __shfl(bmax, (lane - 16) & 63, 64), e2 = __shfl(bmax, (lane - 32) & 63, 64),
-                       e3 = __shfl(bmax, (lane - 48) & 63, 64);
-        unsigned cur0 = m;
-        if (grp >= 1) cur0 = max(cur0, e1);
-        if (grp >= 2) cur0 = max(cur0, e2);
-        if (grp >= 3) cur0 = max(cur0, e3);
-        // weights and rescale factors: one exp per key, no branches, so the
-        // 16 table reads can be in flight together
-        unsigned xs[16];
-        unsigned recm = 0u;  // bit k: key k is a record
-        unsigned M = cur0;
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const unsigned s = sv[k];
-            const bool rec = s > M;
-            unsigned x;
-            if (GEN) {
-                const int d = rec ? (int)(M - s) : (int)(s - M);  // i32 wrap, as the reference
-                x = d >= 0 ? 65535u : exp_neg(0u - (unsigned)d, lut32);
-            } else {
-                x = exp_neg(max(s, M) - min(s, M), lut32);
-            }
-            // a record over "nothing seen" (biased 0) has no rescale; in the fast
-            // path only the lane's first key can meet M == 0 as a record
-            if (GEN || k == 0) x = (rec && M == 0u) ? 0u : x;
-            xs[k] = x;
-            recm |= (rec ? 1u : 0u) << k;
-            M = max(M, s);
-        }
-        // records before this lane's keys in the row
-        const int nrec = __builtin_popcount(recm);
-        const int r1 = __shfl(nrec, (lane - 16) & 63, 64), r2 = __shfl(nrec, (lane - 32) & 63, 64),
-                  r3 = __shfl(nrec, (lane - 48) & 63, 64);
-        int seg = (grp >= 1 ? r1 : 0) + (grp >= 2 ? r2 : 0) + (grp >= 3 ? r3 : 0);
-        // rescale factors of the records, segment ids and weights as signed
-        // byte pairs; byte k of a dword = key 16*grp + 4*i + k
-        unsigned hi_dw[4], lo_dw[4], sg_dw[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            unsigned w4[4];
-            unsigned sg = 0u;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const bool rec = (recm >> (i * 4 + k)) & 1u;
-                if (rec) {
-                    W.rec_e[row][seg] = (uint16_t)xs[i * 4 + k];
-                    seg++;
-                }
-                w4[k] = rec ? 65535u : xs[i * 4 + k];
-                sg |= (unsigned)seg << (8 * k);
-            }
-            const unsigned p01 = __builtin_amdgcn_perm(w4[1], w4[0], 0x05010400u);
-            const unsigned p23 = __builtin_amdgcn_perm(w4[3], w4[2], 0x05010400u);
-            lo_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;
-            hi_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
-            sg_dw[i] = sg;
-        }
-        if (diag) {  // keys after the row: weight 0 (bytes 0x80), no segment (0xFF)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int q = nvalid - 4 * i;
-                const unsigned vm = q >= 4 ? 0xFFFFFFFFu : (q <= 0 ? 0u : ((1u << (8 * q)) - 1u));
-                hi_dw[i] = pick(vm, hi_dw[i], 0x80808080u);
-                lo_dw[i] = pick(vm, lo_dw[i], 0x80808080u);
-                sg_dw[i] = pick(vm, sg_dw[i], 0xFFFFFFFFu);
-            }
-        }
-        {
-            unsigned mr = max(M, (unsigned)__shfl_xor((int)M, 16, 64));
-            m = max(mr, (unsigned)__shfl_xor((int)mr, 32, 64));
-        }
-        int nrow = nrec + __shfl_xor(nrec, 16, 64);
-        nrow += __shfl_xor(nrow, 32, 64);
-
-        // 3. segment j of every row in pass j (MFMA column = row): O_j^T = V^T P_j^T
-        if (grp == 0) W.nrec[row] = nrow;
-        int nmax = nrow;
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
-        // A operand of the PV product: V^T row (head dim 16*db + lane % 16), keys 16*grp .. +16
-        v4i vop[4];
-#pragma unroll
-        for (int db = 0; db < 4; db++) vop[db] = *(const v4i*)(Vt + (db * 16 + row) * KLD + grp * 16);
-        // 32896 * sum over the tile's 64 keys of v[key][dim = lane]
-        unsigned corr;
-        {
-            const int* vrow = (const int*)(Vt + lane * KLD);
-            int cs = 0;
-#pragma unroll
-            for (int i = 0; i < 16; i++) cs = __builtin_amdgcn_sdot4(vrow[i], 0x01010101, cs, false);
-            corr = (unsigned)cs * WOFF;
-        }
-        wave_lds_fence();
-        int nr[16];
-#pragma unroll
-        for (int r = 0; r < 16; r++) nr[r] = __builtin_amdgcn_readfirstlane(W.nrec[r]);
-        for (int j = 0; j <= nmax; j++) {
-            const unsigned jb = (unsigned)j * 0x01010101u;
-            v4i bh, bl;
-            int sh = 0, sl = 0;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const unsigned msk = zero_bytes_mask(sg_dw[i] ^ jb);
-                bh[i] = (int)pick(msk, hi_dw[i], 0x80808080u);
-                bl[i] = (int)pick(msk, lo_dw[i], 0x80808080u);
-                sh = __builtin_amdgcn_sdot4(bh[i], 0x01010101, sh, false);
-                sl = __builtin_amdgcn_sdot4(bl[i], 0x01010101, sl, false);
-            }
-            int sw = sh * 256 + sl;  // sum over this lane's 16 keys of (w_j - 32896)
-            sw += __shfl_xor(sw, 16, 64);
-            sw += __shfl_xor(sw, 32, 64);
-            // rescale factor of this lane's row at record j (0: none); row r's is
-            // read by the combine from lane r
-            const unsigned erow = (j >= 1 && j <= nrow) ? (unsigned)W.rec_e[row][j - 1] : 0u;
-            // 4a. S of this lane's row (lanes = rows): rescale at record j, then add segment j
-            if (erow) S = rescale_s64(S, erow);
-            S += (unsigned)sw + 64u * WOFF;
-#pragma unroll
-            for (int db = 0; db < 4; db++) {
-                v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[db], bh, (v4i){0, 0, 0, 0}, 0, 0, 0);
-                acc = acc << 8;
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[db], bl, acc, 0, 0, 0);
-                *(int4*)&W.buf[row][db * 16 + grp * 4] = make_int4(acc[0], acc[1], acc[2], acc[3]);
-            }
-            wave_lds_fence();
-            // 4b. vacc (lanes = head dims): every row that has a segment j
-            unsigned bv[16];
-#pragma unroll
-            for (int r = 0; r < 16; r++) bv[r] = W.buf[r][lane];
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                if (j <= nr[r]) {
-                    const unsigned e = (unsigned)__builtin_amdgcn_readlane((int)erow, r);
-                    if (e) vacc[r] = rescale_v(vacc[r], e);
-                    vacc[r] += bv[r] + corr;
-                }
-            }
-            wave_lds_fence();
-        }
+        attn_tile<GEN>([&](int blk) { return *(const v4i*)(Ks + (blk * 16 + row) * KLD + grp * 16); },
+                       [&](int db) { return *(const v4i*)(Vt + (db * 16 + row) * KLD + grp * 16); }, qop, mscale,
+                       nvalid, t0 + 63 > wrow0, 16, lut32, W, st);
     }
     if (!wave_live) return;
     // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-        const unsigned slo = (unsigned)__shfl((int)(unsigned)S, r, 64);
-        const unsigned shi = (unsigned)__shfl((int)(unsigned)(S >> 32), r, 64);
+        const unsigned slo = (unsigned)__shfl((int)(unsigned)st.S, r, 64);
+        const unsigned shi = (unsigned)__shfl((int)(unsigned)(st.S >> 32), r, 64);
         const int pr = wrow0 + r;
         if (pr < len) {
             const unsigned long long Sr = ((unsigned long long)shi << 32) | slo;
             const unsigned long long den = Sr == 0 ? 1ull : Sr;
-            a.out[((size_t)b * T + pr) * D + h * 64 + lane] = (int8_t)clamp127(div_rne_s32_u64((int)vacc[r], den));
+            a.out[((size_t)b * T + pr) * D + h * 64 + lane] = (int8_t)clamp127(div_rne_s32_u64((int)st.vacc[r], den));
         }
     }
 }

@@ -1,7 +1,7 @@
 // Batched autoregressive decode (decompression): one token per stream per
 // step, each stream a chunk of the .czip payload (main.rs:377-396), with an
 // arithmetic decoder per stream kept on the device (arith_coder.rs:139-264).
-#include "czip_device.h"
+#include "czip_attn_tile.h"
 #include "czip_kernels.h"
 
 namespace czip {
@@ -53,216 +53,116 @@ void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s) 
 
 // ---------------------------------------------------------------------------
 // Decode attention (attention.rs:162-289 for one query per stream): one
-// workgroup per (stream, KV group), one wavefront per head of the group.  Per
-// 64-key tile the K rows and the transposed V (V^T rows, one per head dim)
-// are staged in LDS once for all heads, while the next tile is fetched into
-// registers.  Each wave then:
-//  1. lanes = keys: scores, the running max by a wave prefix max, records,
-//     weights and rescale factors, and the prefix sums of the weights;
-//  2. lanes = head dims: walks the tile in groups of 4 keys; a group's
-//     contribution sum(w v) comes from sdot4 over signed weight bytes
-//     (w - 32896 = 256*hi + lo, plus 32896 * sum(v) of the group), and a
-//     group holding records is split at them: rescale at the record, then
-//     continue (the reference's in-order update, attention.rs:227-276).
-// S follows the same records with segment sums taken from the prefix sums.
-constexpr int DKLD = 80;              // LDS row stride of the K and V^T tiles (conflict-free 16-byte reads)
-constexpr unsigned DWOFF = 32896;     // w - DWOFF = 256*hi + lo with hi, lo signed bytes
-
-__device__ __forceinline__ int dec_score(int dot, double mscale) {
-    // sra_rne64(sra_rne32(dot, 2) * mult, 15) with the i32 clamp: exact in f64
-    const int du = (dot + 1 + ((dot >> 2) & 1)) >> 2;
-    double r = __builtin_rint((double)du * mscale);
-    r = fmin(fmax(r, -2147483648.0), 2147483647.0);
-    return (int)r;
-}
-
-// rescale at a record (attention.rs:246-261): ((i64)v * e +- 2^15) >> 16
-__device__ __forceinline__ unsigned dec_rescale(unsigned v, unsigned e) {
-    const int vh = (int)v >> 16;
-    const unsigned t = __umul24(v & 0xFFFFu, e);
-    return (unsigned)__mul24(vh, (int)e) + (t >> 16) + ((t >> 15) & 1u) + (unsigned)((int)v >> 31);
-}
-
-// sum over the keys of byte mask m (0xFF per key) of w * v for one group of 4
-// keys: weights hi/lo (other keys carry w = 0, i.e. bytes 0x80), values vg
-__device__ __forceinline__ unsigned group_wv(unsigned hi, unsigned lo, unsigned m, int vg, unsigned vsum) {
-    const unsigned h = (hi & m) | (0x80808080u & ~m), l = (lo & m) | (0x80808080u & ~m);
-    const int sh = __builtin_amdgcn_sdot4((int)h, vg, 0, false), sl = __builtin_amdgcn_sdot4((int)l, vg, 0, false);
-    return ((unsigned)sh << 8) + (unsigned)sl + vsum * DWOFF;
-}
-
-__global__ __launch_bounds__(1024) void k_attn_decode(AttnArgs a, int p) {
+// wavefront per (stream, KV group, block of up to 16 of the group's heads),
+// four independent wavefronts per workgroup.  The 16 rows of attn_tile are
+// the heads, all at the stream's position p over the cached keys 0..p.  Each
+// lane loads its own K and V^T operand fragments (16 bytes each) straight
+// from the caches, one tile ahead: the next tile's K right after the score
+// MFMA has consumed the current one, its V^T after the current tile's passes.
+// ---------------------------------------------------------------------------
+template <bool GEN>
+__global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int hblocks) {
     __shared__ unsigned lut32[256];
-    __shared__ __attribute__((aligned(16))) int8_t Ks[64 * DKLD];
-    __shared__ __attribute__((aligned(16))) int8_t Vt[64 * DKLD];
-    __shared__ __attribute__((aligned(16))) uint8_t whi[16][64], wlo[16][64];
-    __shared__ unsigned ekl[16][64];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, nthr = (int)blockDim.x;
-    const int b = blockIdx.x, g = blockIdx.y;
-    for (int i = tid; i < 256; i += nthr) lut32[i] = (unsigned)a.lut[i] << 16;
-    if (p >= a.lens[b]) return;  // stream finished (uniform)
+    __shared__ __attribute__((aligned(16))) AttnWaveLds wl[4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int row = lane & 15, grp = lane >> 4;
+    lut32[tid] = (unsigned)a.lut[tid] << 16;
+    __syncthreads();
+    const int per_stream = a.KH * hblocks;
+    const int item = (int)blockIdx.x * 4 + wave;
+    const int b = item / per_stream;
+    if (b >= a.B || p >= a.lens[b]) return;  // no barrier follows
+    const int g = (item % per_stream) / hblocks, hb = item % hblocks;
     // heads of KV group g: h with (h * G) / H == g in GQA mode; all heads otherwise
     int h0 = 0, h1 = a.H;
     if (a.kv_mode == 1) {
         h0 = (g * a.H + a.G - 1) / a.G;
         h1 = ((g + 1) * a.H + a.G - 1) / a.G;
     }
-    const int h = h0 + wave;
-    const bool live = h < h1;
+    h0 += 16 * hb;
+    const int nrows = min(16, h1 - h0);
+    if (nrows <= 0) return;
+    const bool live = row < nrows;
+    const int h = h0 + (live ? row : 0);
     const int D = a.H * 64;
-    const int8_t* K = a.kc + ((size_t)b * a.KH + g) * a.T * 64;
-    const int8_t* Vr = a.vc + ((size_t)b * a.KH + g) * a.T * 64;
-    const double mscale = live ? (double)a.score_mult[h] * (1.0 / 32768.0) : 0.0;
-    int q4[16];
-    {
-        const int4* qp = (const int4*)(a.q + (size_t)b * D + (live ? h : h0) * 64);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int4 v = qp[i];
-            q4[4 * i] = v.x; q4[4 * i + 1] = v.y; q4[4 * i + 2] = v.z; q4[4 * i + 3] = v.w;
-        }
-    }
-    int m = INT32_MIN;
-    unsigned long long S = 0;
-    unsigned vacc = 0;
-    if (a.sink && live) {  // attention.rs:211-224: the sink score is the initial max, weight E(0)
+    const int8_t* Kg = a.kc + ((size_t)b * a.KH + g) * a.TP * 64;  // [TP][64]
+    const int8_t* Vg = a.vc + ((size_t)b * a.KH + g) * a.TP * 64;  // [TP/16][64][16]
+    const double mscale = (double)a.score_mult[h] * (1.0 / 32768.0);
+    v4i qop = (v4i){0, 0, 0, 0};
+    if (live) qop = *(const v4i*)(a.q + (size_t)b * D + h * 64 + grp * 16);
+
+    AttnRows st;
+    st.m = live ? 0u : 0xFFFFFFFFu;  // rows past the group's heads: never a record
+    st.S = 0;
+    for (int r = 0; r < 16; r++) st.vacc[r] = 0;
+    if (a.sink) {  // attention.rs:211-224: sink score is the initial max, weight E(0) = 65535
+        const int* sk = (const int*)(a.sink + grp * 16);
         int dot = 0;
-#pragma unroll
-        for (int i = 0; i < 16; i++) dot = __builtin_amdgcn_sdot4(q4[i], ((const int*)a.sink)[i], dot, false);
-        m = dec_score(dot, mscale);
-        S = 65535ull;
+        for (int i = 0; i < 4; i++) dot = __builtin_amdgcn_sdot4(qop[i], sk[i], dot, false);
+        dot += __shfl_xor(dot, 16, 64);
+        dot += __shfl_xor(dot, 32, 64);
+        if (live) {
+            st.m = score_b<GEN>(dot, mscale);
+            st.S = 65535ull;
+        }
     }
-    // tile chunks of 16 bytes: 256 of K then 256 of V (key r, dims c .. c+15);
-    // a thread holds chunks tid and tid + nthr (nthr >= 256)
-    int4 pre0 = make_int4(0, 0, 0, 0), pre1 = pre0;
-    auto fetch = [&](int t0) {
-        const int i0 = tid, i1 = tid + nthr;
-        const int8_t* base0 = i0 < 256 ? K : Vr;
-        pre0 = *(const int4*)(base0 + (size_t)(t0 + ((i0 & 255) >> 2)) * 64 + (i0 & 3) * 16);
-        if (i1 < 512) {
-            const int8_t* base1 = i1 < 256 ? K : Vr;
-            pre1 = *(const int4*)(base1 + (size_t)(t0 + ((i1 & 255) >> 2)) * 64 + (i1 & 3) * 16);
-        }
-    };
-    auto stage = [&](int i, int4 v) {
-        const int r = (i & 255) >> 2, c = (i & 3) * 16;
-        if (i < 256) {
-            *(int4*)(Ks + r * DKLD + c) = v;
-        } else {
-            const int vv[4] = {v.x, v.y, v.z, v.w};
+
+    const int ntiles = p / 64 + 1;  // keys 0..p; tile t0 + 64 <= p stays inside TP
+    v4i kop[4], vop[4];
 #pragma unroll
-            for (int k = 0; k < 16; k++) Vt[(c + k) * DKLD + r] = (int8_t)(vv[k >> 2] >> (8 * (k & 3)));
-        }
-    };
-    fetch(0);
-    for (int t0 = 0; t0 <= p; t0 += 64) {
-        __syncthreads();
-        stage(tid, pre0);
-        if (tid + nthr < 512) stage(tid + nthr, pre1);
-        __syncthreads();
-        if (t0 + 64 <= p) fetch(t0 + 64);
-        if (!live) continue;
-        const int nt = min(64, p - t0 + 1);
-        // 1. lanes = keys
-        int s = INT32_MIN;
-        if (lane < nt) {
-            const int* k4 = (const int*)(Ks + lane * DKLD);
-            int dot = 0;
+    for (int blk = 0; blk < 4; blk++) kop[blk] = *(const v4i*)(Kg + (size_t)(blk * 16 + row) * 64 + grp * 16);
 #pragma unroll
-            for (int i = 0; i < 16; i++) dot = __builtin_amdgcn_sdot4(q4[i], k4[i], dot, false);
-            s = dec_score(dot, mscale);
-        }
-        int pm = s;
+    for (int db = 0; db < 4; db++) vop[db] = *(const v4i*)(Vg + ((size_t)grp * 64 + db * 16 + row) * 16);
+    for (int kt = 0; kt < ntiles; kt++) {
+        const int t0 = kt * 64;
+        const bool more = kt + 1 < ntiles;
+        int nvalid = p - (t0 + grp * 16) + 1;
+        nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
+        attn_tile<GEN>(
+            [&](int blk) {
+                const v4i k = kop[blk];
+                if (more) kop[blk] = *(const v4i*)(Kg + (size_t)(t0 + 64 + blk * 16 + row) * 64 + grp * 16);
+                return k;
+            },
+            [&](int db) { return vop[db]; }, qop, mscale, nvalid, t0 + 63 > p, nrows, lut32, wl[wave], st);
+        if (more) {
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int v = __shfl_up(pm, o, 64);
-            if (lane >= o) pm = max(pm, v);
+            for (int db = 0; db < 4; db++)
+                vop[db] = *(const v4i*)(Vg + ((size_t)((t0 + 64) / 16 + grp) * 64 + db * 16 + row) * 16);
         }
-        pm = max(pm, m);
-        int prev = __shfl_up(pm, 1, 64);
-        if (lane == 0) prev = m;
-        const bool rec = lane < nt && s > prev;
-        unsigned w = 0, e = 0;
-        if (lane < nt) {
-            const unsigned x = exp_q16_bf(rec ? (int)((unsigned)prev - (unsigned)s) : (int)((unsigned)s - (unsigned)pm),
-                                          lut32, ATTN_COEF_Q24);
-            w = rec ? 65535u : x;
-            e = (rec && prev != INT32_MIN) ? x : 0u;
-        }
-        unsigned pw = w;  // inclusive prefix sum of the weights (< 2^22)
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const unsigned v = (unsigned)__shfl_up((int)pw, o, 64);
-            if (lane >= o) pw += v;
-        }
-        const unsigned pe = pw - w;  // exclusive
-        const unsigned long long recm = __ballot(rec);
-        const unsigned wx = w ^ 0x8080u;
-        whi[wave][lane] = (uint8_t)(wx >> 8);
-        wlo[wave][lane] = (uint8_t)wx;
-        ekl[wave][lane] = e;
-        m = __shfl(pm, 63, 64);
-        const unsigned total = (unsigned)__shfl((int)pw, 63, 64);
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        // 2. lanes = head dims
-        int vr[16];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int4 v = *(const int4*)(Vt + lane * DKLD + 16 * i);
-            vr[4 * i] = v.x; vr[4 * i + 1] = v.y; vr[4 * i + 2] = v.z; vr[4 * i + 3] = v.w;
-        }
-        const unsigned* hw = (const unsigned*)whi[wave];
-        const unsigned* lw = (const unsigned*)wlo[wave];
-        int cur = 0;  // first key of the running segment
-#pragma unroll
-        for (int gi = 0; gi < 16; gi++) {
-            const unsigned vsum = (unsigned)__builtin_amdgcn_sdot4(vr[gi], 0x01010101, 0, false);
-            const unsigned rb = (unsigned)(recm >> (4 * gi)) & 0xFu;
-            if (rb == 0u) {
-                vacc += group_wv(hw[gi], lw[gi], 0xFFFFFFFFu, vr[gi], vsum);
-            } else {
-                unsigned from = 0;  // first key of the group not yet added
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    if ((rb >> r) & 1u) {
-                        const unsigned mk = (r > 0 ? (0xFFFFFFFFu >> (32 - 8 * r)) : 0u) & ~((1u << (8 * from)) - 1u);
-                        vacc += group_wv(hw[gi], lw[gi], mk, vr[gi], vsum);
-                        const int kr = 4 * gi + r;
-                        const unsigned ej = ekl[wave][kr];
-                        S += (unsigned)__builtin_amdgcn_readlane((int)pe, kr) - (unsigned)__builtin_amdgcn_readlane((int)pe, cur);
-                        if (ej) {
-                            vacc = dec_rescale(vacc, ej);
-                            S = (S * ej + 0x8000ull) >> 16;
-                        }
-                        cur = kr;
-                        from = (unsigned)r;
-                    }
-                }
-                vacc += group_wv(hw[gi], lw[gi], ~((1u << (8 * from)) - 1u), vr[gi], vsum);
-            }
-        }
-        S += total - (unsigned)__builtin_amdgcn_readlane((int)pe, cur);
     }
-    if (!live) return;
-    const unsigned long long den = S == 0 ? 1ull : S;
-    a.out[(size_t)b * D + h * 64 + lane] = (int8_t)clamp127(div_rne_s32_u64((int)vacc, den));
+    // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const unsigned slo = (unsigned)__shfl((int)(unsigned)st.S, r, 64);
+        const unsigned shi = (unsigned)__shfl((int)(unsigned)(st.S >> 32), r, 64);
+        if (r < nrows) {
+            const unsigned long long Sr = ((unsigned long long)shi << 32) | slo;
+            const unsigned long long den = Sr == 0 ? 1ull : Sr;
+            a.out[(size_t)b * D + (h0 + r) * 64 + lane] = (int8_t)clamp127(div_rne_s32_u64((int)st.vacc[r], den));
+        }
+    }
 }
 
 void launch_attn_decode(const AttnArgs& a, int S, int p, hipStream_t s) {
-    // waves per workgroup: the most heads any KV group has
-    const int KH = a.KH;
-    int waves = a.H;
+    // head blocks per KV group: the most heads any group has, 16 per wavefront
+    int heads = a.H;
     if (a.kv_mode == 1) {
-        waves = 0;
-        for (int g = 0; g < KH; g++) {
+        heads = 0;
+        for (int g = 0; g < a.KH; g++) {
             const int h0 = (g * a.H + a.G - 1) / a.G, h1 = ((g + 1) * a.H + a.G - 1) / a.G;
-            waves = h1 - h0 > waves ? h1 - h0 : waves;
+            heads = h1 - h0 > heads ? h1 - h0 : heads;
         }
     }
-    // at least 4 waves: the tile staging gives each thread at most 2 of the
-    // 512 16-byte chunks of a K + V tile
-    if (waves < 4) waves = 4;
-    hipLaunchKernelGGL(k_attn_decode, dim3((unsigned)S, (unsigned)KH), dim3(64 * waves), 0, s, a, p);
+    const int hblocks = (heads + 15) / 16;
+    AttnArgs g = a;
+    g.B = S;
+    const long long items = (long long)S * a.KH * hblocks;
+    dim3 grid((unsigned)((items + 3) / 4));
+    if (a.general)
+        hipLaunchKernelGGL(k_attn_decode<true>, grid, dim3(256), 0, s, g, p, hblocks);
+    else
+        hipLaunchKernelGGL(k_attn_decode<false>, grid, dim3(256), 0, s, g, p, hblocks);
 }
 
 // ---------------------------------------------------------------------------

@@ -206,19 +206,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
                     int8_t* k = a.kc + (((size_t)b * a.KH + g) * a.T + p) * 64;
                     *(unsigned*)(k + i0) = pack4i(xq[0], xq[1], xq[2], xq[3]);
                     *(unsigned*)(k + i0 + 32) = pack4i(yq[0], yq[1], yq[2], yq[3]);
-                } else if (a.pos >= 0) {
-                    // V of a decode step: key-major like K (one contiguous row per
-                    // stream; the decode attention transposes its tiles in LDS)
-                    int8_t* v = a.vc + (((size_t)b * a.KH + g) * a.T + p) * 64;
-                    *(unsigned*)(v + i0) = pack4i(xv[0], xv[1], xv[2], xv[3]);
-                    *(unsigned*)(v + i0 + 32) = pack4i(yv[0], yv[1], yv[2], yv[3]);
                 } else {
-                    // V, stored dim-major for the prefill PV operand
-                    int8_t* v = a.vc + (((size_t)b * a.KH + g) * 64) * a.TP + p;
+                    // V^T in blocks of 16 keys, [key/16][dim][16]: the PV operand
+                    // of both attention kernels is 16 consecutive keys of one dim
+                    int8_t* v = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP + (size_t)(p >> 4) * 1024 + (p & 15);
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        v[(size_t)(i0 + r) * a.TP] = (int8_t)xv[r];
-                        v[(size_t)(i0 + r + 32) * a.TP] = (int8_t)yv[r];
+                        v[(i0 + r) * 16] = (int8_t)xv[r];
+                        v[(i0 + r + 32) * 16] = (int8_t)yv[r];
                     }
                 }
             }

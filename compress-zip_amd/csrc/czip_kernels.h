@@ -26,9 +26,9 @@ struct GemmArgs {
     int rq_fast;      // 1: |acc * mult| < 2^53, requant by one f64 multiply and rint
     // EPI_QKV
     int d, T, kv_mode, G, KH;
-    int TP;           // V^T row stride: T rounded up to a multiple of 64
+    int TP;           // keys per V^T block: T rounded up to a multiple of 64
     int8_t* kc;       // [B, KH, T, 64]   rotated keys
-    int8_t* vc;       // [B, KH, 64, TP]  values, transposed (dim-major); decode: [B, KH, T, 64]
+    int8_t* vc;       // [B, KH, TP/16, 64, 16]  values, transposed in blocks of 16 keys
     int pos;          // >= 0: every row is at this position and row = chunk (decode step)
     const int16_t* rcos;
     const int16_t* rsin;
@@ -37,7 +37,7 @@ struct GemmArgs {
 struct AttnArgs {
     const int8_t* q;          // [M, H*64]  rotated + NET_SHIFT-ed queries
     const int8_t* kc;         // [B, KH, T, 64]
-    const int8_t* vc;         // [B, KH, 64, TP]
+    const int8_t* vc;         // [B, KH, TP/16, 64, 16]
     int TP;
     const int32_t* lens;      // [B]
     const int32_t* score_mult;// [H]
