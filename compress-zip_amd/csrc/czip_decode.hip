@@ -53,35 +53,34 @@ void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s) 
 
 // ---------------------------------------------------------------------------
 // Decode attention (attention.rs:162-289 for one query per stream): one
-// wavefront per (stream, KV group, block of up to 16 of the group's heads),
-// four independent wavefronts per workgroup.  The 16 rows of attn_tile are
+// wavefront per (stream, KV group), four independent wavefronts per
+// workgroup (d_model <= 1024 bounds a group to 16 heads).  The 16 rows of attn_tile are
 // the heads, all at the stream's position p over the cached keys 0..p.  Each
 // lane loads its own K and V^T operand fragments (16 bytes each) straight
-// from the caches, one tile ahead: the next tile's K right after the score
-// MFMA has consumed the current one, its V^T after the current tile's passes.
+// from the caches, one tile ahead, into a second register set.
 // ---------------------------------------------------------------------------
+// word 3 of a raw buffer resource on gfx9 parts: 32-bit data format, no swizzle
+constexpr int BUF_DWORD3 = 0x00020000;
+
 template <bool GEN>
-__global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int hblocks) {
+__global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p) {
     __shared__ unsigned lut32[256];
     __shared__ __attribute__((aligned(16))) AttnWaveLds wl[4];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: stream, group and caches in SGPRs
     const int row = lane & 15, grp = lane >> 4;
     lut32[tid] = (unsigned)a.lut[tid] << 16;
     __syncthreads();
-    const int per_stream = a.KH * hblocks;
     const int item = (int)blockIdx.x * 4 + wave;
-    const int b = item / per_stream;
+    const int b = item / a.KH, g = item % a.KH;
     if (b >= a.B || p >= a.lens[b]) return;  // no barrier follows
-    const int g = (item % per_stream) / hblocks, hb = item % hblocks;
     // heads of KV group g: h with (h * G) / H == g in GQA mode; all heads otherwise
     int h0 = 0, h1 = a.H;
     if (a.kv_mode == 1) {
         h0 = (g * a.H + a.G - 1) / a.G;
         h1 = ((g + 1) * a.H + a.G - 1) / a.G;
     }
-    h0 += 16 * hb;
-    const int nrows = min(16, h1 - h0);
-    if (nrows <= 0) return;
+    const int nrows = h1 - h0;
     const bool live = row < nrows;
     const int h = h0 + (live ? row : 0);
     const int D = a.H * 64;
@@ -108,29 +107,43 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int h
     }
 
     const int ntiles = p / 64 + 1;  // keys 0..p; tile t0 + 64 <= p stays inside TP
-    v4i kop[4], vop[4];
+    // operands of tile t0 in one register set while the next tile's are loaded
+    // into the other; the last tile reloads itself, so the loads stay
+    // unconditional and nothing waits on them before their use
+    // (buffer loads: one 32-bit offset per lane, range-checked against the
+    // stream's TP * 64 bytes)
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)Kg, (short)0, a.TP * 64, BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)Vg, (short)0, a.TP * 64, BUF_DWORD3);
+    auto load_k = [&](v4i* k, int blk, int t) {
+        k[blk] = __builtin_amdgcn_raw_buffer_load_b128(rk, (t + blk * 16 + row) * 64 + grp * 16, 0, 0);
+    };
+    auto load_v = [&](v4i* v, int t) {
 #pragma unroll
-    for (int blk = 0; blk < 4; blk++) kop[blk] = *(const v4i*)(Kg + (size_t)(blk * 16 + row) * 64 + grp * 16);
-#pragma unroll
-    for (int db = 0; db < 4; db++) vop[db] = *(const v4i*)(Vg + ((size_t)grp * 64 + db * 16 + row) * 16);
-    for (int kt = 0; kt < ntiles; kt++) {
-        const int t0 = kt * 64;
-        const bool more = kt + 1 < ntiles;
+        for (int db = 0; db < 4; db++)
+            v[db] = __builtin_amdgcn_raw_buffer_load_b128(rv, ((t / 16 + grp) * 64 + db * 16 + row) * 16, 0, 0);
+    };
+    auto tile = [&](v4i* kc, v4i* vc, v4i* kn, v4i* vn, int t0) {
+        const int tn = t0 + 64 <= p ? t0 + 64 : t0;
         int nvalid = p - (t0 + grp * 16) + 1;
         nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
         attn_tile<GEN>(
             [&](int blk) {
-                const v4i k = kop[blk];
-                if (more) kop[blk] = *(const v4i*)(Kg + (size_t)(t0 + 64 + blk * 16 + row) * 64 + grp * 16);
-                return k;
+                load_k(kn, blk, tn);
+                return kc[blk];
             },
-            [&](int db) { return vop[db]; }, qop, mscale, nvalid, t0 + 63 > p, nrows, lut32, wl[wave], st);
-        if (more) {
+            [&](int db) { return vc[db]; }, qop, mscale, nvalid, t0 + 63 > p, nrows, lut32, wl[wave], st);
+        load_v(vn, tn);
+    };
+    v4i k0[4], v0[4], k1[4], v1[4];
 #pragma unroll
-            for (int db = 0; db < 4; db++)
-                vop[db] = *(const v4i*)(Vg + ((size_t)((t0 + 64) / 16 + grp) * 64 + db * 16 + row) * 16);
-        }
+    for (int blk = 0; blk < 4; blk++) load_k(k0, blk, 0);
+    load_v(v0, 0);
+    int kt = 0;
+    for (; kt + 1 < ntiles; kt += 2) {
+        tile(k0, v0, k1, v1, kt * 64);
+        tile(k1, v1, k0, v0, kt * 64 + 64);
     }
+    if (kt < ntiles) tile(k0, v0, k1, v1, kt * 64);
     // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r
 #pragma unroll
     for (int r = 0; r < 16; r++) {
@@ -145,24 +158,14 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int h
 }
 
 void launch_attn_decode(const AttnArgs& a, int S, int p, hipStream_t s) {
-    // head blocks per KV group: the most heads any group has, 16 per wavefront
-    int heads = a.H;
-    if (a.kv_mode == 1) {
-        heads = 0;
-        for (int g = 0; g < a.KH; g++) {
-            const int h0 = (g * a.H + a.G - 1) / a.G, h1 = ((g + 1) * a.H + a.G - 1) / a.G;
-            heads = h1 - h0 > heads ? h1 - h0 : heads;
-        }
-    }
-    const int hblocks = (heads + 15) / 16;
+    // a.H <= 16 (d_model <= 1024): every KV group fits one wavefront's rows
     AttnArgs g = a;
     g.B = S;
-    const long long items = (long long)S * a.KH * hblocks;
-    dim3 grid((unsigned)((items + 3) / 4));
+    dim3 grid((unsigned)(((long long)S * a.KH + 3) / 4));
     if (a.general)
-        hipLaunchKernelGGL(k_attn_decode<true>, grid, dim3(256), 0, s, g, p, hblocks);
+        hipLaunchKernelGGL(k_attn_decode<true>, grid, dim3(256), 0, s, g, p);
     else
-        hipLaunchKernelGGL(k_attn_decode<false>, grid, dim3(256), 0, s, g, p, hblocks);
+        hipLaunchKernelGGL(k_attn_decode<false>, grid, dim3(256), 0, s, g, p);
 }
 
 // ---------------------------------------------------------------------------

@@ -293,6 +293,47 @@ def test_decompress_random_models(amd, orc, random_models):
         assert np.array_equal(gm.decompress_chunks(chunks, ntoks), toks)
 
 
+def _roundtrip(amd, orc, path, kv, toks, chunk):
+    gm, om = _model_pair(amd, orc, path, kv)
+    ref = om.compress_many(toks, chunk, threads=8)
+    assert gm.compress_chunks(toks, chunk) == ref
+    ntoks = [min(chunk, toks.size - c * chunk) for c in range(len(ref))]
+    assert np.array_equal(gm.decompress_chunks(ref, ntoks), toks)
+
+
+def test_decompress_attention_edge_cases(amd, orc, tmp_path):
+    """Decode attention beyond the plain models: 16 query heads on one KV head
+    (all 16 rows of a wavefront live), the general path (clamped, wrapping
+    scores; lut[0] != 65535; a sink) and rows where nearly every key is a
+    record; each coded by the oracle and decoded on the device."""
+    from czip_amd import synth
+    path = synth.write_random_model(str(tmp_path / "mqa16.czm"), d=1024, n_layers=1, n_heads=16, n_kv=1, d_ff=256,
+                                    vocab=1024, ctx=256, seed=95)
+    _say("decompress 16 heads on one KV head")
+    _roundtrip(amd, orc, path, amd.KV_GQA, synth.zipf_ids(80 * 2 + 33, 1024, seed=96), 80)
+
+    t, meta = synth.random_model_tensors(d=256, n_layers=1, n_heads=4, n_kv=1, d_ff=256, vocab=1024, ctx=256,
+                                         seed=51, sink=True)
+    t["layers.0.attn.score_mult"] = np.array([1 << 30, -(1 << 30), 1 << 27, -5], np.int32)
+    lut = t["lut.exp2"].copy()
+    lut[0] = 65000
+    t["lut.exp2"] = lut
+    path = _write_model(str(tmp_path / "gen.czm"), t, meta)
+    _say("decompress general attention path")
+    _roundtrip(amd, orc, path, amd.KV_RUST_COMPAT, synth.zipf_ids(150 + 41, 1024, seed=97), 150)
+
+    d, vocab, T = 256, 1024, 256
+    t, meta = synth.random_model_tensors(d=d, n_layers=1, n_heads=4, n_kv=1, d_ff=256, vocab=vocab, ctx=T, seed=70)
+    t["embed.weight"], t["layers.0.attn_norm.weight"], t["layers.0.attn.qkv.weight"] = record_stress_weights(d, vocab)
+    t["layers.0.attn.qkv.shift"] = np.array(17, np.int8)
+    t["lut.rope_cos"] = np.full_like(t["lut.rope_cos"], 32767)
+    t["lut.rope_sin"] = np.zeros_like(t["lut.rope_sin"])
+    path = _write_model(str(tmp_path / "records.czm"), t, meta)
+    toks = np.concatenate([np.arange(0, vocab, vocab // 200)[:200], np.arange(0, 131) * 7]).astype(np.uint32)
+    _say("decompress every-key-a-record")
+    _roundtrip(amd, orc, path, amd.KV_RUST_COMPAT, toks, 200)
+
+
 def test_decompress_stream_groups(gpu_shipped, shipped, monkeypatch):
     """More chunks than streams per group: groups run one after the other."""
     monkeypatch.setenv("CZIP_DECODE_STREAMS", "3")
