@@ -18,7 +18,8 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) int8_t Vt[64 * KLD];
     __shared__ __attribute__((aligned(16))) AttnWaveLds wl[4];
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row = lane & 15, grp = lane >> 4;
     // 1-D grid, XCD-aware: workgroups go round-robin over the 8 XCDs; XCD x
     // takes chunks x, x + 8, ..., all (query block, head) pairs of a chunk in a
@@ -46,7 +47,7 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     if (p < T) qop = *(const v4i*)(a.q + ((size_t)b * T + p) * D + h * 64 + grp * 16);
 
     AttnRows st;
-    st.m = 0u;
+    st.m = INT32_MIN;
     st.S = 0;
     for (int r = 0; r < 16; r++) st.vacc[r] = 0;
     if (a.sink) {  // attention.rs:211-224: sink score is the initial max, weight E(0) = 65535
@@ -61,22 +62,23 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
 
     const int ntiles = (min(q0 + 63, len - 1)) / 64 + 1;
     // K / V^T tile of 64 keys: thread -> row tid/4, 16 bytes; V^T is stored
-    // in blocks of 16 keys ([key/16][dim][16])
+    // in blocks of 16 keys ([key/16][dim][16]).  Buffer loads: the tile offset
+    // is uniform, and keys past T read as 0 (the resource's range check).
     const int ldr = tid >> 2, ldc = (tid & 3) * 16;
-    int4 kreg = make_int4(0, 0, 0, 0), vreg;
-    if (ldr < T) kreg = *(const int4*)(Kg + (size_t)ldr * 64 + ldc);
-    vreg = *(const int4*)(Vg + ((size_t)(ldc >> 4) * 64 + ldr) * 16);
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)Kg, (short)0, T * 64, BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)Vg, (short)0, a.TP * 64, BUF_DWORD3);
+    const int koff = ldr * 64 + ldc, voff = (ldc >> 4) * 1024 + ldr * 16;
+    v4i kreg = __builtin_amdgcn_raw_buffer_load_b128(rk, koff, 0, 0);
+    v4i vreg = __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0);
     for (int kt = 0; kt < ntiles; kt++) {
         const int t0 = kt * 64;
         __syncthreads();
-        *(int4*)(Ks + ldr * KLD + ldc) = kreg;
-        *(int4*)(Vt + ldr * KLD + ldc) = vreg;
+        *(v4i*)(Ks + ldr * KLD + ldc) = kreg;
+        *(v4i*)(Vt + ldr * KLD + ldc) = vreg;
         __syncthreads();
         if (kt + 1 < ntiles) {
-            const int t1 = t0 + 64;
-            kreg = make_int4(0, 0, 0, 0);
-            if (t1 + ldr < T) kreg = *(const int4*)(Kg + (size_t)(t1 + ldr) * 64 + ldc);
-            vreg = *(const int4*)(Vg + ((size_t)((t1 + ldc) >> 4) * 64 + ldr) * 16);
+            kreg = __builtin_amdgcn_raw_buffer_load_b128(rk, koff, (t0 + 64) * 64, 0);
+            vreg = __builtin_amdgcn_raw_buffer_load_b128(rv, voff, (t0 + 64) * 64, 0);
         }
         if (!wave_live || t0 > wave_last) continue;
         int nvalid = p - (t0 + grp * 16) + 1;  // keys t <= p are visible (causal)

@@ -22,8 +22,8 @@
 //  4. hands O_j through LDS to a "lanes = head dims" layout and walks each
 //     row's own segments: rescale at the record, then add (rows with fewer
 //     records skip the pass with a scalar branch); S is kept with lanes = rows.
-// Scores are kept as s ^ 2^31 so that unsigned order is signed order; 0 is
-// INT32_MIN, the reference's "nothing seen yet".
+// INT32_MIN is the reference's "nothing seen yet" max (the fast path's scores
+// stay inside +-2^30, so no score equals it).
 #pragma once
 
 #include "czip_device.h"
@@ -32,27 +32,27 @@ namespace czip {
 
 constexpr int KLD = 80;               // LDS row stride (bytes) of staged K and V^T tiles
 constexpr unsigned WOFF = 32896;      // w - WOFF spans [-32896, 32639] = 256*[-128,127] + [-128,127]
-constexpr unsigned BIAS = 0x80000000u;
 constexpr int RS = 68;                // row stride (words) of the per-wave buffer: 16-byte accesses of 16 rows hit 64 banks
+constexpr int BUF_DWORD3 = 0x00020000;  // word 3 of a raw buffer resource: 32-bit data format, no swizzle
 
 struct AttnWaveLds {
     unsigned buf[16][RS];    // scores [row][key]; then per pass: column sums [column][dim]
-    uint16_t rec_e[16][64];  // rescale factor at record j+1 of row r (0: nothing to rescale)
+    uint16_t ex[16][64];     // [row][key]: at a record key, the rescale factor (0: nothing to rescale)
     int nrec[16];            // records of each row in the tile
 };
 
 __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
-// sra_rne64(sra_rne32(dot, 2) * mult, 15) (attention.rs:233-239), biased.
+// sra_rne64(sra_rne32(dot, 2) * mult, 15) (attention.rs:233-239).
 // RNE of a quotient by 2^k is symmetric, so the floor form
 // (x + 2^(k-1) - 1 + bit_k(x)) >> k equals the reference's sign-magnitude one;
 // the product is exact in f64 and rint rounds half to even.
 template <bool GEN>
-__device__ __forceinline__ unsigned score_b(int dot, double mscale) {
+__device__ __forceinline__ int score_b(int dot, double mscale) {
     const int du = (dot + 1 + ((dot >> 2) & 1)) >> 2;
     double r = __builtin_rint((double)du * mscale);
     if (GEN) r = fmin(fmax(r, -2147483648.0), 2147483647.0);
-    return (unsigned)(int)r ^ BIAS;
+    return (int)r;
 }
 
 // exp_q16(-neg) (lut.rs:213-235) with the table pre-shifted by 16 bits.
@@ -89,11 +89,11 @@ __device__ __forceinline__ unsigned zero_bytes_mask(unsigned x) {
 
 __device__ __forceinline__ unsigned pick(unsigned msk, unsigned a, unsigned b) { return (a & msk) | (b & ~msk); }
 
-// Running state of a wave's 16 rows: max m (biased) and weight sum S with
+// Running state of a wave's 16 rows: max m and weight sum S with
 // lanes = rows (replicated over the 4 lane groups); vacc with lanes = head
 // dims, register index = row.
 struct AttnRows {
-    unsigned m;
+    int m;
     unsigned long long S;
     unsigned vacc[16];
 };
@@ -113,29 +113,29 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
 #pragma unroll
     for (int blk = 0; blk < 4; blk++) {
         v4i sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(blk), qop, (v4i){0, 0, 0, 0}, 0, 0, 0);
-        *(uint4*)&W.buf[row][blk * 16 + grp * 4] = make_uint4(score_b<GEN>(sc[0], mscale), score_b<GEN>(sc[1], mscale),
-                                                              score_b<GEN>(sc[2], mscale), score_b<GEN>(sc[3], mscale));
+        *(int4*)&W.buf[row][blk * 16 + grp * 4] = make_int4(score_b<GEN>(sc[0], mscale), score_b<GEN>(sc[1], mscale),
+                                                            score_b<GEN>(sc[2], mscale), score_b<GEN>(sc[3], mscale));
     }
     wave_lds_fence();
 
     // 2. in-order scan of keys [16*grp, 16*grp+16) of this row
-    unsigned sv[16];
+    int sv[16];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const uint4 v = *(const uint4*)&W.buf[row][grp * 16 + i * 4];
+        const int4 v = *(const int4*)&W.buf[row][grp * 16 + i * 4];
         sv[i * 4] = v.x; sv[i * 4 + 1] = v.y; sv[i * 4 + 2] = v.z; sv[i * 4 + 3] = v.w;
     }
     if (diag) {
 #pragma unroll
         for (int k = 0; k < 16; k++)
-            if (k >= nvalid) sv[k] = 0u;  // INT32_MIN: never a record; weight masked below
+            if (k >= nvalid) sv[k] = INT32_MIN;  // never a record; weight masked below
     }
-    unsigned bmax = 0u;
+    int bmax = INT32_MIN;
 #pragma unroll
     for (int k = 0; k < 16; k++) bmax = max(bmax, sv[k]);
-    const unsigned e1 = __shfl(bmax, (lane - 16) & 63, 64), e2 = __shfl(bmax, (lane - 32) & 63, 64),
-                   e3 = __shfl(bmax, (lane - 48) & 63, 64);
-    unsigned cur0 = st.m;
+    const int e1 = __shfl(bmax, (lane - 16) & 63, 64), e2 = __shfl(bmax, (lane - 32) & 63, 64),
+              e3 = __shfl(bmax, (lane - 48) & 63, 64);
+    int cur0 = st.m;
     if (grp >= 1) cur0 = max(cur0, e1);
     if (grp >= 2) cur0 = max(cur0, e2);
     if (grp >= 3) cur0 = max(cur0, e3);
@@ -143,52 +143,60 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
     // 16 table reads can be in flight together
     unsigned xs[16];
     unsigned recm = 0u;  // bit k: key k is a record
-    unsigned M = cur0;
+    int M = cur0;
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-        const unsigned s = sv[k];
+        const int s = sv[k];
         const bool rec = s > M;
         unsigned x;
         if (GEN) {
-            const int d = rec ? (int)(M - s) : (int)(s - M);  // i32 wrap, as the reference
+            const int d = (int)(rec ? (unsigned)M - (unsigned)s : (unsigned)s - (unsigned)M);  // i32 wrap, as the reference
             x = d >= 0 ? 65535u : exp_neg(0u - (unsigned)d, lut32);
         } else {
-            x = exp_neg(max(s, M) - min(s, M), lut32);
+            x = exp_neg((unsigned)max(s, M) - (unsigned)min(s, M), lut32);
         }
-        // a record over "nothing seen" (biased 0) has no rescale; in the fast
-        // path only the lane's first key can meet M == 0 as a record
-        if (GEN || k == 0) x = (rec && M == 0u) ? 0u : x;
+        // a record over "nothing seen" has no rescale; in the fast path only
+        // the lane's first key can meet M == INT32_MIN as a record (masked
+        // keys are a suffix)
+        if (GEN || k == 0) x = (rec && M == INT32_MIN) ? 0u : x;
         xs[k] = x;
         recm |= (rec ? 1u : 0u) << k;
         M = max(M, s);
     }
-    // records before this lane's keys in the row
-    const int nrec = __builtin_popcount(recm);
-    const int r1 = __shfl(nrec, (lane - 16) & 63, 64), r2 = __shfl(nrec, (lane - 32) & 63, 64),
-              r3 = __shfl(nrec, (lane - 48) & 63, 64);
-    int seg = (grp >= 1 ? r1 : 0) + (grp >= 2 ? r2 : 0) + (grp >= 3 ? r3 : 0);
-    // rescale factors of the records, segment ids and weights as signed
-    // byte pairs; byte k of a dword = key 16*grp + 4*i + k
+    // the row's records in the tile (bit = key), its record count and the
+    // records before this lane's keys
+    const unsigned g0 = (unsigned)__shfl((int)recm, row, 64), g1 = (unsigned)__shfl((int)recm, row + 16, 64),
+                   g2 = (unsigned)__shfl((int)recm, row + 32, 64), g3 = (unsigned)__shfl((int)recm, row + 48, 64);
+    unsigned rlo = g0 | (g1 << 16), rhi = g2 | (g3 << 16);
+    const int nrow = __builtin_popcount(rlo) + __builtin_popcount(rhi);
+    const unsigned blo = grp == 0 ? 0u : (grp == 1 ? 0xFFFFu : 0xFFFFFFFFu), bhi = grp == 3 ? 0xFFFFu : 0u;
+    const unsigned seg = (unsigned)(__builtin_popcount(rlo & blo) + __builtin_popcount(rhi & bhi));
+    // every key's factor, read at its record's pass
+    {
+        uint4 e0, e1v;
+        e0.x = xs[0] | (xs[1] << 16); e0.y = xs[2] | (xs[3] << 16); e0.z = xs[4] | (xs[5] << 16); e0.w = xs[6] | (xs[7] << 16);
+        e1v.x = xs[8] | (xs[9] << 16); e1v.y = xs[10] | (xs[11] << 16); e1v.z = xs[12] | (xs[13] << 16);
+        e1v.w = xs[14] | (xs[15] << 16);
+        *(uint4*)&W.ex[row][grp * 16] = e0;
+        *(uint4*)&W.ex[row][grp * 16 + 8] = e1v;
+    }
+    // weights as signed byte pairs (a record's weight is 65535) and segment
+    // ids (records up to and including the key); byte k of a dword = key
+    // 16*grp + 4*i + k
     unsigned hi_dw[4], lo_dw[4], sg_dw[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         unsigned w4[4];
-        unsigned sg = 0u;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const bool rec = (recm >> (i * 4 + k)) & 1u;
-            if (rec) {
-                W.rec_e[row][seg] = (uint16_t)xs[i * 4 + k];
-                seg++;
-            }
-            w4[k] = rec ? 65535u : xs[i * 4 + k];
-            sg |= (unsigned)seg << (8 * k);
-        }
+        for (int k = 0; k < 4; k++) w4[k] = ((recm >> (i * 4 + k)) & 1u) ? 65535u : xs[i * 4 + k];
         const unsigned p01 = __builtin_amdgcn_perm(w4[1], w4[0], 0x05010400u);
         const unsigned p23 = __builtin_amdgcn_perm(w4[3], w4[2], 0x05010400u);
         lo_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;
         hi_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
-        sg_dw[i] = sg;
+        const unsigned nib = (recm >> (4 * i)) & 15u;
+        const unsigned ones = (nib * 0x204081u) & 0x01010101u;  // bit k of nib -> byte k
+        const unsigned base = seg + (unsigned)__builtin_popcount(recm & ((1u << (4 * i)) - 1u));
+        sg_dw[i] = ones * 0x01010101u + base * 0x01010101u;
     }
     if (diag) {  // invisible keys: weight 0 (bytes 0x80), no segment (0xFF)
 #pragma unroll
@@ -201,11 +209,9 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
         }
     }
     {
-        const unsigned mr = max(M, (unsigned)__shfl_xor((int)M, 16, 64));
-        st.m = max(mr, (unsigned)__shfl_xor((int)mr, 32, 64));
+        const int mr = max(M, __shfl_xor(M, 16, 64));
+        st.m = max(mr, __shfl_xor(mr, 32, 64));
     }
-    int nrow = nrec + __shfl_xor(nrec, 16, 64);
-    nrow += __shfl_xor(nrow, 32, 64);
 
     // 3. segment j of every row in pass j (MFMA column = row): O_j^T = V^T P_j^T
     if (grp == 0) W.nrec[row] = nrow;
@@ -242,9 +248,15 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
         int sw = sh * 256 + sl;  // sum over this lane's 16 keys of (w_j - 32896)
         sw += __shfl_xor(sw, 16, 64);
         sw += __shfl_xor(sw, 32, 64);
-        // rescale factor of this lane's row at record j (0: none); row r's is
-        // read by the combine from lane r
-        const unsigned erow = (j >= 1 && j <= nrow) ? (unsigned)W.rec_e[row][j - 1] : 0u;
+        // rescale factor of this lane's row at record j (0: none), the lowest
+        // record not yet passed; row r's is read by the combine from lane r
+        unsigned erow = 0u;
+        if (j >= 1) {
+            const int key = rlo ? __builtin_ctz(rlo) : 32 + __builtin_ctz(rhi | 0x80000000u);
+            erow = j <= nrow ? (unsigned)W.ex[row][key] : 0u;
+            rhi = rlo ? rhi : rhi & (rhi - 1u);
+            rlo &= rlo - 1u;
+        }
         // 4a. S of this lane's row (lanes = rows): rescale at record j, then add segment j
         if (erow) st.S = rescale_s64(st.S, erow);
         st.S += (unsigned)sw + 64u * WOFF;

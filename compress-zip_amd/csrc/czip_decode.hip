@@ -59,9 +59,6 @@ void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s) 
 // lane loads its own K and V^T operand fragments (16 bytes each) straight
 // from the caches, one tile ahead, into a second register set.
 // ---------------------------------------------------------------------------
-// word 3 of a raw buffer resource on gfx9 parts: 32-bit data format, no swizzle
-constexpr int BUF_DWORD3 = 0x00020000;
-
 template <bool GEN>
 __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p) {
     __shared__ unsigned lut32[256];
@@ -91,7 +88,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p) {
     if (live) qop = *(const v4i*)(a.q + (size_t)b * D + h * 64 + grp * 16);
 
     AttnRows st;
-    st.m = live ? 0u : 0xFFFFFFFFu;  // rows past the group's heads: never a record
+    st.m = live ? INT32_MIN : INT32_MAX;  // rows past the group's heads: never a record
     st.S = 0;
     for (int r = 0; r < 16; r++) st.vacc[r] = 0;
     if (a.sink) {  // attention.rs:211-224: sink score is the initial max, weight E(0) = 65535
