@@ -215,6 +215,8 @@ czip_status check_config(czip_ctx* c, const czip_model_desc& w) {
     if (w.exp2_len != 256) return fail(c, CZIP_E_FORMAT, "Exp2 LUT must have exactly 256 entries (lut.rs:57-64)");
     if (w.context_length < 1 || w.rope_len != (int64_t)w.context_length * 32)
         return fail(c, CZIP_E_FORMAT, "RoPE LUT arrays size mismatch with max_seq_len * half_dim (lut.rs:148-165)");
+    if (w.context_length > 65535)
+        return fail(c, CZIP_E_CONFIG, "context_length > 65535 unsupported (the attention sum S is held in 32 bits)");
     if ((uint64_t)w.target_total <= (uint64_t)w.vocab) return fail(c, CZIP_E_CONFIG, "target_total must exceed vocab");
     return CZIP_OK;
 }

@@ -57,7 +57,7 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
         dot += __shfl_xor(dot, 16, 64);
         dot += __shfl_xor(dot, 32, 64);
         st.m = score_b<GEN>(dot, mscale);
-        st.S = 65535ull;
+        st.S = 65535u;
     }
 
     const int ntiles = (min(q0 + 63, len - 1)) / 64 + 1;
@@ -91,12 +91,10 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-        const unsigned slo = (unsigned)__shfl((int)(unsigned)st.S, r, 64);
-        const unsigned shi = (unsigned)__shfl((int)(unsigned)(st.S >> 32), r, 64);
+        const unsigned Sr = (unsigned)__shfl((int)st.S, r, 64);
         const int pr = wrow0 + r;
         if (pr < len) {
-            const unsigned long long Sr = ((unsigned long long)shi << 32) | slo;
-            const unsigned long long den = Sr == 0 ? 1ull : Sr;
+            const unsigned long long den = Sr == 0u ? 1ull : (unsigned long long)Sr;
             a.out[((size_t)b * T + pr) * D + h * 64 + lane] = (int8_t)clamp127(div_rne_s32_u64((int)st.vacc[r], den));
         }
     }

@@ -67,17 +67,18 @@ __device__ __forceinline__ unsigned exp_neg(unsigned neg, const unsigned* lut32)
     return max(x, 1u);
 }
 
-// vacc rescale at a record (attention.rs:246-261): ((i64)v * e +- 2^15) >> 16,
-// formed from 16-bit halves of v with 24-bit multiplies (e in 1..65535).
+// vacc rescale at a record (attention.rs:246-261): the low 32 bits of
+// ((i64)v * e + (v >= 0 ? 2^15 : -2^15)) >> 16 (one 32x32+64 multiply-add)
 __device__ __forceinline__ unsigned rescale_v(unsigned v, unsigned e) {
-    const int vh = (int)v >> 16;
-    const unsigned t = __umul24(v & 0xFFFFu, e);
-    return (unsigned)__mul24(vh, (int)e) + (t >> 16) + ((t >> 15) & 1u) + (unsigned)((int)v >> 31);
+    const int c = (int)v >= 0 ? 0x8000 : -0x8000;
+    return (unsigned)(((long long)(int)v * (long long)(int)e + (long long)c) >> 16);
 }
 
-// S rescale at a record (attention.rs:246-250): (S * e + 0x8000) >> 16
-__device__ __forceinline__ unsigned long long rescale_s64(unsigned long long S, unsigned e) {
-    return (S * e + 0x8000ull) >> 16;
+// S rescale at a record (attention.rs:246-250): (S * e + 0x8000) >> 16.  S is
+// a sum of at most T + 1 weights <= 65535 (rescales only shrink it), so it
+// fits 32 bits for T < 65536; the product is formed in 64.
+__device__ __forceinline__ unsigned rescale_s(unsigned S, unsigned e) {
+    return (unsigned)(((unsigned long long)S * e + 0x8000ull) >> 16);
 }
 
 // bytes of x equal to zero -> 0xFF, others -> 0x00 (exact per byte)
@@ -94,7 +95,7 @@ __device__ __forceinline__ unsigned pick(unsigned msk, unsigned a, unsigned b) {
 // dims, register index = row.
 struct AttnRows {
     int m;
-    unsigned long long S;
+    unsigned S;
     unsigned vacc[16];
 };
 
@@ -142,7 +143,8 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
     // weights and rescale factors: one exp per key, no branches, so the
     // 16 table reads can be in flight together
     unsigned xs[16];
-    unsigned recm = 0u;  // bit k: key k is a record
+    unsigned recm = 0u;   // bit k: key k is a record (weight 65535)
+    unsigned fresh = 0u;  // bit k: key k is a record over "nothing seen": no rescale, no split
     int M = cur0;
 #pragma unroll
     for (int k = 0; k < 16; k++) {
@@ -158,20 +160,27 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
         // a record over "nothing seen" has no rescale; in the fast path only
         // the lane's first key can meet M == INT32_MIN as a record (masked
         // keys are a suffix)
-        if (GEN || k == 0) x = (rec && M == INT32_MIN) ? 0u : x;
+        if (GEN || k == 0) {
+            const bool f = rec && M == INT32_MIN;
+            x = f ? 0u : x;
+            fresh |= (f ? 1u : 0u) << k;
+        }
         xs[k] = x;
         recm |= (rec ? 1u : 0u) << k;
         M = max(M, s);
     }
-    // the row's records in the tile (bit = key), its record count and the
-    // records before this lane's keys
-    const unsigned g0 = (unsigned)__shfl((int)recm, row, 64), g1 = (unsigned)__shfl((int)recm, row + 16, 64),
-                   g2 = (unsigned)__shfl((int)recm, row + 32, 64), g3 = (unsigned)__shfl((int)recm, row + 48, 64);
+    // segments split at the records that rescale (a record over "nothing
+    // seen" has nothing before it to rescale, so its segment runs on): the
+    // row's splits in the tile (bit = key), their count and the splits before
+    // this lane's keys
+    const unsigned splm = recm & ~fresh;
+    const unsigned g0 = (unsigned)__shfl((int)splm, row, 64), g1 = (unsigned)__shfl((int)splm, row + 16, 64),
+                   g2 = (unsigned)__shfl((int)splm, row + 32, 64), g3 = (unsigned)__shfl((int)splm, row + 48, 64);
     unsigned rlo = g0 | (g1 << 16), rhi = g2 | (g3 << 16);
     const int nrow = __builtin_popcount(rlo) + __builtin_popcount(rhi);
     const unsigned blo = grp == 0 ? 0u : (grp == 1 ? 0xFFFFu : 0xFFFFFFFFu), bhi = grp == 3 ? 0xFFFFu : 0u;
     const unsigned seg = (unsigned)(__builtin_popcount(rlo & blo) + __builtin_popcount(rhi & bhi));
-    // every key's factor, read at its record's pass
+    // every key's factor, read at its split's pass
     {
         uint4 e0, e1v;
         e0.x = xs[0] | (xs[1] << 16); e0.y = xs[2] | (xs[3] << 16); e0.z = xs[4] | (xs[5] << 16); e0.w = xs[6] | (xs[7] << 16);
@@ -181,7 +190,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
         *(uint4*)&W.ex[row][grp * 16 + 8] = e1v;
     }
     // weights as signed byte pairs (a record's weight is 65535) and segment
-    // ids (records up to and including the key); byte k of a dword = key
+    // ids (splits up to and including the key); byte k of a dword = key
     // 16*grp + 4*i + k
     unsigned hi_dw[4], lo_dw[4], sg_dw[4];
 #pragma unroll
@@ -193,9 +202,9 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
         const unsigned p23 = __builtin_amdgcn_perm(w4[3], w4[2], 0x05010400u);
         lo_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;
         hi_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
-        const unsigned nib = (recm >> (4 * i)) & 15u;
+        const unsigned nib = (splm >> (4 * i)) & 15u;
         const unsigned ones = (nib * 0x204081u) & 0x01010101u;  // bit k of nib -> byte k
-        const unsigned base = seg + (unsigned)__builtin_popcount(recm & ((1u << (4 * i)) - 1u));
+        const unsigned base = seg + (unsigned)__builtin_popcount(splm & ((1u << (4 * i)) - 1u));
         sg_dw[i] = ones * 0x01010101u + base * 0x01010101u;
     }
     if (diag) {  // invisible keys: weight 0 (bytes 0x80), no segment (0xFF)
@@ -258,7 +267,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
             rlo &= rlo - 1u;
         }
         // 4a. S of this lane's row (lanes = rows): rescale at record j, then add segment j
-        if (erow) st.S = rescale_s64(st.S, erow);
+        if (erow) st.S = rescale_s(st.S, erow);
         st.S += (unsigned)sw + 64u * WOFF;
 #pragma unroll
         for (int db = 0; db < 4; db++) {

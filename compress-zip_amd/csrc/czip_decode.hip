@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p) {
         dot += __shfl_xor(dot, 32, 64);
         if (live) {
             st.m = score_b<GEN>(dot, mscale);
-            st.S = 65535ull;
+            st.S = 65535u;
         }
     }
 
@@ -144,11 +144,9 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p) {
     // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-        const unsigned slo = (unsigned)__shfl((int)(unsigned)st.S, r, 64);
-        const unsigned shi = (unsigned)__shfl((int)(unsigned)(st.S >> 32), r, 64);
+        const unsigned Sr = (unsigned)__shfl((int)st.S, r, 64);
         if (r < nrows) {
-            const unsigned long long Sr = ((unsigned long long)shi << 32) | slo;
-            const unsigned long long den = Sr == 0 ? 1ull : Sr;
+            const unsigned long long den = Sr == 0u ? 1ull : (unsigned long long)Sr;
             a.out[(size_t)b * D + (h0 + r) * 64 + lane] = (int8_t)clamp127(div_rne_s32_u64((int)st.vacc[r], den));
         }
     }
