@@ -37,8 +37,12 @@ template <class G>
 void set_requant(G& g, int mult, int shift) {
     g.mult = mult;
     g.shift = shift;
+    // fast path: |acc * mult| < 2^53 (exact in f64) and |acc * mult * 2^-shift|
+    // < 2^31 (the FMA rint's low word), with |acc| <= K * 127 * 128
     const long long am = mult < 0 ? -(long long)mult : (long long)mult;
-    g.rq_fast = (am < (1ll << 26) && shift <= 62 && g.K <= 8192) ? 1 : 0;
+    const double accmax = (double)g.K * 127.0 * 128.0;
+    const double ymax = shift <= 0 ? accmax * (double)am : ldexp(accmax * (double)am, -shift);
+    g.rq_fast = (am < (1ll << 26) && shift <= 62 && g.K <= 8192 && ymax < 2147483648.0) ? 1 : 0;
     g.rq_scale = shift <= 0 ? (double)mult : ldexp((double)mult, -shift);
 }
 

@@ -47,11 +47,13 @@ __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOM
 // RNE of a quotient by 2^k is symmetric, so the floor form
 // (x + 2^(k-1) - 1 + bit_k(x)) >> k equals the reference's sign-magnitude one;
 // the product is exact in f64 and rint rounds half to even.
+// The fast path (|score| < 2^30) takes the rint from one FMA.
 template <bool GEN>
 __device__ __forceinline__ int score_b(int dot, double mscale) {
     const int du = (dot + 1 + ((dot >> 2) & 1)) >> 2;
+    if (!GEN) return rint_fma_i32((double)du, mscale);
     double r = __builtin_rint((double)du * mscale);
-    if (GEN) r = fmin(fmax(r, -2147483648.0), 2147483647.0);
+    r = fmin(fmax(r, -2147483648.0), 2147483647.0);
     return (int)r;
 }
 

@@ -18,6 +18,15 @@ constexpr uint32_t BOS_TOKEN = 1022u;        // main.rs:222, 387
 
 __device__ __forceinline__ int clamp127(int x) { return x < -127 ? -127 : (x > 127 ? 127 : x); }
 
+// rint(a * b) (round half to even) for |a * b| < 2^31, exact when a * b is
+// exact in f64: adding 1.5 * 2^52 makes the ulp 1, so the FMA's single
+// rounding lands on the integer, and the low word of the sum is that integer
+// modulo 2^32 (the mantissa holds 2^51 + rint(a * b)).
+__device__ __forceinline__ int rint_fma_i32(double a, double b) {
+    const double r = __builtin_fma(a, b, 6755399441055744.0);
+    return (int)(unsigned)__builtin_bit_cast(unsigned long long, r);
+}
+
 // primitives.rs:18-42
 __device__ __forceinline__ int sra_rne32(int v, unsigned sh) {
     if (sh == 0) return v;

@@ -43,14 +43,11 @@ __device__ __forceinline__ void store_tile(const TileRegs& t, int8_t* lds, int t
 }
 
 // model.rs:280-300.  Fast path: |v * mult| < 2^53, so v * mult * 2^-shift is
-// exact in f64 and rint rounds half to even like sra_rne_tte_s64_to_s32.
+// exact in f64, and |v * mult * 2^-shift| < 2^31, so its rint (half to even,
+// like sra_rne_tte_s64_to_s32) is one FMA and the clamp an integer med3.
 template <bool FAST>
 __device__ __forceinline__ int rq(int v, double scale, int mult, int shift) {
-    if (FAST) {
-        double x = __builtin_rint((double)v * scale);
-        x = fmin(fmax(x, -127.0), 127.0);
-        return (int)x;
-    }
+    if (FAST) return clamp127(rint_fma_i32((double)v, scale));
     return requant(v, mult, shift);
 }
 template <bool FAST>

@@ -23,7 +23,7 @@ struct GemmArgs {
     int ldo;
     int mult, shift;
     double rq_scale;  // mult * 2^-shift (mult when shift <= 0), used when rq_fast
-    int rq_fast;      // 1: |acc * mult| < 2^53, requant by one f64 multiply and rint
+    int rq_fast;      // 1: |acc * mult| < 2^53 and |acc * rq_scale| < 2^31: requant by one f64 FMA
     // EPI_QKV
     int d, T, kv_mode, G, KH;
     int TP;           // keys per V^T block: T rounded up to a multiple of 64
