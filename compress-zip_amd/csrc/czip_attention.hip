@@ -14,8 +14,8 @@ namespace czip {
 template <bool GEN>
 __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     __shared__ unsigned lut32[256];
-    __shared__ __attribute__((aligned(16))) int8_t Ks[64 * KLD];
-    __shared__ __attribute__((aligned(16))) int8_t Vt[64 * KLD];
+    __shared__ __attribute__((aligned(16))) int8_t Ks[64 * 64];
+    __shared__ __attribute__((aligned(16))) int8_t Vt[64 * 64];
     __shared__ __attribute__((aligned(16))) AttnWaveLds wl[4];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -73,8 +73,8 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     for (int kt = 0; kt < ntiles; kt++) {
         const int t0 = kt * 64;
         __syncthreads();
-        *(v4i*)(Ks + ldr * KLD + ldc) = kreg;
-        *(v4i*)(Vt + ldr * KLD + ldc) = vreg;
+        *(v4i*)(Ks + lds64(ldr, tid & 3)) = kreg;
+        *(v4i*)(Vt + lds64(ldr, tid & 3)) = vreg;
         __syncthreads();
         if (kt + 1 < ntiles) {
             kreg = __builtin_amdgcn_raw_buffer_load_b128(rk, koff, (t0 + 64) * 64, 0);
@@ -83,8 +83,8 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
         if (!wave_live || t0 > wave_last) continue;
         int nvalid = p - (t0 + grp * 16) + 1;  // keys t <= p are visible (causal)
         nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
-        attn_tile<GEN>([&](int blk) { return *(const v4i*)(Ks + (blk * 16 + row) * KLD + grp * 16); },
-                       [&](int db) { return *(const v4i*)(Vt + (db * 16 + row) * KLD + grp * 16); }, qop, mscale,
+        attn_tile<GEN>([&](int blk) { return *(const v4i*)(Ks + lds64(blk * 16 + row, grp)); },
+                       [&](int db) { return *(const v4i*)(Vt + lds64(db * 16 + row, grp)); }, qop, mscale,
                        nvalid, t0 + 63 > wrow0, 16, lut32, W, st);
     }
     if (!wave_live) return;

@@ -30,7 +30,6 @@
 
 namespace czip {
 
-constexpr int KLD = 80;               // LDS row stride (bytes) of staged K and V^T tiles
 constexpr unsigned WOFF = 32896;      // w - WOFF spans [-32896, 32639] = 256*[-128,127] + [-128,127]
 constexpr int RS = 68;                // row stride (words) of the per-wave buffer: 16-byte accesses of 16 rows hit 64 banks
 constexpr int BUF_DWORD3 = 0x00020000;  // word 3 of a raw buffer resource: 32-bit data format, no swizzle

@@ -18,6 +18,14 @@ constexpr uint32_t BOS_TOKEN = 1022u;        // main.rs:222, 387
 
 __device__ __forceinline__ int clamp127(int x) { return x < -127 ? -127 : (x > 127 ? 127 : x); }
 
+// Byte offset of 16-byte chunk c of row r in an LDS tile of 64-byte rows, the
+// chunks of a row permuted by c ^ ((r >> 1) & 3): both the MFMA operand reads
+// (lane -> row l % 16, chunk l / 16) and the row-major stores (lane -> row
+// l / 4, chunk l % 4) then touch every bank once per access (measured with
+// the LDS bank-conflict counter on gfx950; an unpermuted 80-byte stride costs
+// 4 extra cycles per read and 8 per store).
+__device__ __forceinline__ int lds64(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
+
 // rint(a * b) (round half to even) for |a * b| < 2^31, exact when a * b is
 // exact in f64: adding 1.5 * 2^52 makes the ulp 1, so the FMA's single
 // rounding lands on the integer, and the low word of the sum is that integer

@@ -15,31 +15,31 @@ namespace czip {
 // output columns 4*(l/16) .. +3 (consecutive) of row l % 16 of each 16x16
 // tile, and the epilogues store 4 outputs with one vector store.
 // ---------------------------------------------------------------------------
-constexpr int BM = 128, BN = 128, BK = 64, LDSK = BK + 16;
+constexpr int BM = 128, BN = 128, BK = 64;
 constexpr int NXCD = 8;  // XCDs of an MI355X
 
 struct TileRegs {
-    int4 v[2];
+    v4i v[2];
 };
 
-__device__ __forceinline__ void fetch_tile(const int8_t* __restrict__ src, int rows_total, int ld, int row0, int k0,
-                                           int tid, TileRegs& t) {
-    // 128 rows x 64 bytes: thread t -> row t/2, bytes (t%2)*32 .. +32
-    const int r = tid >> 1, c = (tid & 1) * 32;
-    t.v[0] = make_int4(0, 0, 0, 0);
-    t.v[1] = t.v[0];
-    if (row0 + r < rows_total) {
-        const int4* g = (const int4*)(src + (size_t)(row0 + r) * ld + k0 + c);
-        t.v[0] = g[0];
-        t.v[1] = g[1];
-    }
+constexpr int BUF_DWORD3 = 0x00020000;  // word 3 of a raw buffer resource: 32-bit data format, no swizzle
+
+// The rows [row0, row0 + 128) of a row-major [rows_total, ld] int8 matrix as a
+// buffer resource: rows past rows_total read as 0 (range check).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const int8_t* src, int rows_total, int ld, int row0) {
+    const int rows = min(rows_total - row0, 128);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(src + (size_t)row0 * ld), (short)0, rows * ld, BUF_DWORD3);
+}
+
+// 128 rows x 64 bytes at column k0: thread t -> rows t/4 and t/4 + 64, chunk t%4
+__device__ __forceinline__ void fetch_tile(__amdgpu_buffer_rsrc_t r, int voff, int voff2, int k0, TileRegs& t) {
+    t.v[0] = __builtin_amdgcn_raw_buffer_load_b128(r, voff, k0, 0);
+    t.v[1] = __builtin_amdgcn_raw_buffer_load_b128(r, voff2, k0, 0);
 }
 
 __device__ __forceinline__ void store_tile(const TileRegs& t, int8_t* lds, int tid) {
-    const int r = tid >> 1, c = (tid & 1) * 32;
-    int4* l = (int4*)(lds + r * LDSK + c);
-    l[0] = t.v[0];
-    l[1] = t.v[1];
+    *(v4i*)(lds + lds64(tid >> 2, tid & 3)) = t.v[0];
+    *(v4i*)(lds + lds64((tid >> 2) + 64, tid & 3)) = t.v[1];
 }
 
 // model.rs:280-300.  Fast path: |v * mult| < 2^53, so v * mult * 2^-shift is
@@ -61,8 +61,8 @@ __device__ __forceinline__ unsigned pack4i(int a, int b, int c, int d) {
 
 template <int EPI, bool FAST>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t As[2][BM * LDSK];
-    __shared__ __attribute__((aligned(16))) int8_t Ws[2][BN * LDSK];
+    __shared__ __attribute__((aligned(16))) int8_t As[2][BM * 64];
+    __shared__ __attribute__((aligned(16))) int8_t Ws[2][BN * 64];
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
@@ -81,23 +81,26 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
         for (int j = 0; j < 4; j++) acc[i][j] = (v4i){0, 0, 0, 0};
 
     TileRegs ta, tw;
-    fetch_tile(a.A, a.M, a.K, m0, 0, tid, ta);
-    fetch_tile(a.W, a.N, a.K, n0, 0, tid, tw);
+    const __amdgpu_buffer_rsrc_t ra = tile_rsrc(a.A, a.M, a.K, m0), rw = tile_rsrc(a.W, a.N, a.K, n0);
+    const int voff = (tid >> 2) * a.K + (tid & 3) * 16, voff2 = voff + 64 * a.K;
+    fetch_tile(ra, voff, voff2, 0, ta);
+    fetch_tile(rw, voff, voff2, 0, tw);
     store_tile(ta, As[0], tid);
     store_tile(tw, Ws[0], tid);
     __syncthreads();
     const int lr = lane & 15, lk = (lane >> 4) * 16;
     for (int kt = 0; kt < nk; kt++) {
         const int cur = kt & 1;
-        if (kt + 1 < nk) {
-            fetch_tile(a.A, a.M, a.K, m0, (kt + 1) * BK, tid, ta);
-            fetch_tile(a.W, a.N, a.K, n0, (kt + 1) * BK, tid, tw);
+        if (kt + 1 < nk) {  // the next K step, fetched while this one is multiplied
+            fetch_tile(ra, voff, voff2, (kt + 1) * BK, ta);
+            fetch_tile(rw, voff, voff2, (kt + 1) * BK, tw);
         }
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of this step's MFMAs
         v4i af[4], bf[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[cur] + (wm * 64 + i * 16 + lr) * LDSK + lk);
+        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[cur] + lds64(wm * 64 + i * 16 + lr, lane >> 4));
 #pragma unroll
-        for (int j = 0; j < 4; j++) bf[j] = *(const v4i*)(Ws[cur] + (wn * 64 + j * 16 + lr) * LDSK + lk);
+        for (int j = 0; j < 4; j++) bf[j] = *(const v4i*)(Ws[cur] + lds64(wn * 64 + j * 16 + lr, lane >> 4));
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -259,7 +262,7 @@ __device__ __forceinline__ int rms_el(int x, int w, int inv) { return clamp127(r
 
 template <int NW, int CT, bool FAST>
 __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t As[2][RBM * LDSK];
+    __shared__ __attribute__((aligned(16))) int8_t As[2][RBM * 64];
     __shared__ unsigned red[NW][RBM];
     __shared__ int inv_s[RBM];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -282,7 +285,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
         if (tid < 256 && m0 + ar < a.M) ra = *(const int4*)(a.A + (size_t)(m0 + ar) * a.K + k0 + ac);
     };
     auto store_a = [&](int buf) {
-        if (tid < 256) *(int4*)(As[buf] + ar * LDSK + ac) = ra;
+        if (tid < 256) *(int4*)(As[buf] + lds64(ar, tid & 3)) = ra;
     };
     v4i wf[CT];
     auto fetch_w = [&](int k0) {
@@ -304,7 +307,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
         }
         v4i af[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[cur] + (i * 16 + lr) * LDSK + lk);
+        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[cur] + lds64(i * 16 + lr, lane >> 4));
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll

@@ -19,11 +19,11 @@ namespace czip {
 // Lane l holds logits of rows 16 i + l % 16 (i < 4) at columns
 // 16 t + 4 (l / 16) .. +3 of its wave's range (t < CT).
 // ---------------------------------------------------------------------------
-constexpr int HBM_ROWS = 64, HBK = 64, HLDSK = HBK + 16, HNW = 16;
+constexpr int HBM_ROWS = 64, HBK = 64, HNW = 16;
 
 template <int CT>
 __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t As[2][HBM_ROWS * HLDSK];
+    __shared__ __attribute__((aligned(16))) int8_t As[2][HBM_ROWS * 64];
     __shared__ unsigned lut32[256];
     __shared__ int red_a[HNW][HBM_ROWS];
     __shared__ unsigned red_b[HNW][HBM_ROWS], red_c[HNW][HBM_ROWS];
@@ -50,7 +50,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
         if (tid < 256 && m0 + ar < a.M) ra = *(const int4*)(a.A + (size_t)(m0 + ar) * a.K + k0 + ac);
     };
     auto store_a = [&](int buf) {
-        if (tid < 256) *(int4*)(As[buf] + ar * HLDSK + ac) = ra;
+        if (tid < 256) *(int4*)(As[buf] + lds64(ar, tid & 3)) = ra;
     };
     v4i wf[CT];
     auto fetch_w = [&](int k0) {
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
         }
         v4i af[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[cur] + (i * 16 + lr) * HLDSK + lk);
+        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[cur] + lds64(i * 16 + lr, lane >> 4));
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
