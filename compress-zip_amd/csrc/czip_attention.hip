@@ -83,9 +83,9 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
         if (!wave_live || t0 > wave_last) continue;
         int nvalid = p - (t0 + grp * 16) + 1;  // keys t <= p are visible (causal)
         nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
-        attn_tile<GEN>([&](int blk) { return *(const v4i*)(Ks + lds64(blk * 16 + row, grp)); },
-                       [&](int db) { return *(const v4i*)(Vt + lds64(db * 16 + row, grp)); }, qop, mscale,
-                       nvalid, t0 + 63 > wrow0, 16, lut32, W, st);
+        attn_tile<GEN, 1>([&](int, int blk) { return *(const v4i*)(Ks + lds64(blk * 16 + row, grp)); },
+                          [&](int, int db) { return *(const v4i*)(Vt + lds64(db * 16 + row, grp)); }, [] {}, &qop, 0,
+                          16, mscale, nvalid, t0 + 63 > wrow0, 16, lut32, W, st);
     }
     if (!wave_live) return;
     // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r

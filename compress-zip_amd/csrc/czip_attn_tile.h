@@ -100,24 +100,37 @@ struct AttnRows {
     unsigned vacc[16];
 };
 
-// One 64-key tile.  kop(blk): the K operand of keys 16*blk + lane%16, head
-// dims 16*(lane/16) .. +16; vop(db): the V^T operand of head dim
-// 16*db + lane%16, keys 16*(lane/16) .. +16 (both called once per index).
+// One 64-key tile.  kop(s, blk): the K operand of keys 16*blk + lane%16,
+// head dims 16*(lane/16) .. +16; vop(s, db): the V^T operand of head dim
+// 16*db + lane%16, keys 16*(lane/16) .. +16 (each called once per index);
+// after_scores() runs once the score products have consumed every K operand.
 // nvalid: keys [16*(lane/16), +nvalid) of the lane's row are visible (the
 // others get weight 0 and are never records), used when diag is set; rows
 // >= nrows are not combined into vacc (their m, S and vacc are unused).
-template <bool GEN, class KOp, class VOp>
-__device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double mscale, int nvalid, bool diag,
-                                          int nrows, const unsigned* lut32, AttnWaveLds& W, AttnRows& st) {
+//
+// NS > 1 packs NS independent key streams (decode: streams sharing nothing
+// but the shape) into the wave's rows: rows [s*G, s*G + G) read stream s.
+// Every product is then summed over the streams with the other streams' rows
+// zeroed in the row-side operand (qs[s]: the lane's query when its row reads
+// stream s, else 0; rs: the lane's row's stream), so each row meets only its
+// own stream's keys and values: the streams are consecutive slices of the
+// contraction.  NS == 1: qs[0] is the query operand, rs and G are unused.
+template <bool GEN, int NS, class KOp, class VOp, class After>
+__device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scores, const v4i* qs, int rs, int G,
+                                          double mscale, int nvalid, bool diag, int nrows, const unsigned* lut32,
+                                          AttnWaveLds& W, AttnRows& st) {
     const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
 
     // 1. S^T = K Q^T, score epilogue, stored [row][key]
 #pragma unroll
     for (int blk = 0; blk < 4; blk++) {
-        v4i sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(blk), qop, (v4i){0, 0, 0, 0}, 0, 0, 0);
+        v4i sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(0, blk), qs[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+        for (int t = 1; t < NS; t++) sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(t, blk), qs[t], sc, 0, 0, 0);
         *(int4*)&W.buf[row][blk * 16 + grp * 4] = make_int4(score_b<GEN>(sc[0], mscale), score_b<GEN>(sc[1], mscale),
                                                             score_b<GEN>(sc[2], mscale), score_b<GEN>(sc[3], mscale));
     }
+    after_scores();
     wave_lds_fence();
 
     // 2. in-order scan of keys [16*grp, 16*grp+16) of this row
@@ -229,17 +242,21 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
     // A operand of the PV product, and the sum over the tile's 64 keys of v
-    // (the product with a column of ones, moved to lanes = head dims)
-    v4i vop[4];
+    // per stream (the product with a column of ones, moved to lanes = head dims)
+    v4i vop[NS][4];
 #pragma unroll
-    for (int db = 0; db < 4; db++) {
-        vop[db] = vop_at(db);
-        const v4i cs = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-            vop[db], (v4i){0x01010101, 0x01010101, 0x01010101, 0x01010101}, (v4i){0, 0, 0, 0}, 0, 0, 0);
-        if (row == 0) *(int4*)&W.buf[0][db * 16 + grp * 4] = make_int4(cs[0], cs[1], cs[2], cs[3]);
-    }
+    for (int t = 0; t < NS; t++)
+#pragma unroll
+        for (int db = 0; db < 4; db++) {
+            vop[t][db] = vop_at(t, db);
+            const v4i cs = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                vop[t][db], (v4i){0x01010101, 0x01010101, 0x01010101, 0x01010101}, (v4i){0, 0, 0, 0}, 0, 0, 0);
+            if (row == 0) *(int4*)&W.buf[t][db * 16 + grp * 4] = make_int4(cs[0], cs[1], cs[2], cs[3]);
+        }
     wave_lds_fence();
-    const unsigned corr = W.buf[0][lane] * WOFF;
+    unsigned corr[NS];
+#pragma unroll
+    for (int t = 0; t < NS; t++) corr[t] = W.buf[t][lane] * WOFF;
     int nr[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) nr[r] = __builtin_amdgcn_readfirstlane(W.nrec[r]);
@@ -270,11 +287,28 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
         // 4a. S of this lane's row (lanes = rows): rescale at record j, then add segment j
         if (erow) st.S = rescale_s(st.S, erow);
         st.S += (unsigned)sw + 64u * WOFF;
+        // the weight columns per stream: the other streams' rows read 0
+        v4i bhs[NS], bls[NS];
+        if (NS == 1) {
+            bhs[0] = bh;
+            bls[0] = bl;
+        } else {
+#pragma unroll
+            for (int t = 0; t < NS; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    bhs[t][i] = rs == t ? bh[i] : 0;
+                    bls[t][i] = rs == t ? bl[i] : 0;
+                }
+        }
 #pragma unroll
         for (int db = 0; db < 4; db++) {
-            v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[db], bh, (v4i){0, 0, 0, 0}, 0, 0, 0);
+            v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[0][db], bhs[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+            for (int t = 1; t < NS; t++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[t][db], bhs[t], acc, 0, 0, 0);
             acc = acc << 8;
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[db], bl, acc, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < NS; t++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[t][db], bls[t], acc, 0, 0, 0);
             *(int4*)&W.buf[row][db * 16 + grp * 4] = make_int4(acc[0], acc[1], acc[2], acc[3]);
         }
         wave_lds_fence();
@@ -288,7 +322,10 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, v4i qop, double m
             if (r < nrows && j <= nr[r]) {
                 const unsigned e = (unsigned)__builtin_amdgcn_readlane((int)erow, r);
                 if (e) st.vacc[r] = rescale_v(st.vacc[r], e);
-                st.vacc[r] += bv[r] + corr;
+                unsigned c = corr[0];
+#pragma unroll
+                for (int t = 1; t < NS; t++) c = r >= t * G ? corr[t] : c;
+                st.vacc[r] += bv[r] + c;
             }
         }
         wave_lds_fence();

@@ -53,42 +53,57 @@ void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s) 
 
 // ---------------------------------------------------------------------------
 // Decode attention (attention.rs:162-289 for one query per stream): one
-// wavefront per (stream, KV group), four independent wavefronts per
-// workgroup (d_model <= 1024 bounds a group to 16 heads).  The 16 rows of attn_tile are
-// the heads, all at the stream's position p over the cached keys 0..p.  Each
-// lane loads its own K and V^T operand fragments (16 bytes each) straight
-// from the caches, one tile ahead, into a second register set.
+// wavefront per (NS streams, KV group), four independent wavefronts per
+// workgroup.  The G heads of the group (d_model <= 1024 bounds G to 16) at
+// the streams' position p are the rows of attn_tile: with 2 * G <= 16, two
+// streams share a wavefront (rows [0, G) and [G, 2G)), each meeting only its
+// own stream's keys.  Each lane loads its own K and V^T operand fragments
+// (16 bytes each) straight from the caches, one tile ahead: one stream into
+// a second register set, two streams in place (K once the scores have used
+// it, V after the tile's passes).
 // ---------------------------------------------------------------------------
-template <bool GEN>
-__global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p) {
+template <bool GEN, int NS>
+__global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a, int p, int G) {
     __shared__ unsigned lut32[256];
     __shared__ __attribute__((aligned(16))) AttnWaveLds wl[4];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: stream, group and caches in SGPRs
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: streams, group and caches in SGPRs
     const int row = lane & 15, grp = lane >> 4;
     lut32[tid] = (unsigned)a.lut[tid] << 16;
     __syncthreads();
     const int item = (int)blockIdx.x * 4 + wave;
-    const int b = item / a.KH, g = item % a.KH;
-    if (b >= a.B || p >= a.lens[b]) return;  // no barrier follows
-    // heads of KV group g: h with (h * G) / H == g in GQA mode; all heads otherwise
-    int h0 = 0, h1 = a.H;
-    if (a.kv_mode == 1) {
-        h0 = (g * a.H + a.G - 1) / a.G;
-        h1 = ((g + 1) * a.H + a.G - 1) / a.G;
+    const int sp = item / a.KH, g = item % a.KH;
+    int bs[NS];
+    bool act[NS], any = false;
+#pragma unroll
+    for (int t = 0; t < NS; t++) {
+        bs[t] = sp * NS + t;
+        act[t] = bs[t] < a.B && p < a.lens[bs[t]];
+        any = any || act[t];
+        bs[t] = min(bs[t], a.B - 1);  // a finished or missing stream's rows are dead; its loads stay in range
     }
-    const int nrows = h1 - h0;
-    const bool live = row < nrows;
-    const int h = h0 + (live ? row : 0);
+    if (!any) return;  // no barrier follows
+    // heads of KV group g: h with (h * G) / H == g in GQA mode; all heads otherwise
+    const int h0 = a.kv_mode == 1 ? (g * a.H + a.G - 1) / a.G : 0;
+    const int rs = NS == 1 ? 0 : min(row / G, NS);  // the row's stream (NS: no stream)
+    bool live = row < NS * G;
+#pragma unroll
+    for (int t = 0; t < NS; t++)
+        if (rs == t) live = live && act[t];
+    int b = bs[0];
+#pragma unroll
+    for (int t = 1; t < NS; t++) b = rs == t ? bs[t] : b;
+    const int h = h0 + (row < NS * G ? row - rs * G : 0);
     const int D = a.H * 64;
-    const int8_t* Kg = a.kc + ((size_t)b * a.KH + g) * a.TP * 64;  // [TP][64]
-    const int8_t* Vg = a.vc + ((size_t)b * a.KH + g) * a.TP * 64;  // [TP/16][64][16]
     const double mscale = (double)a.score_mult[h] * (1.0 / 32768.0);
     v4i qop = (v4i){0, 0, 0, 0};
     if (live) qop = *(const v4i*)(a.q + (size_t)b * D + h * 64 + grp * 16);
+    v4i qs[NS];
+#pragma unroll
+    for (int t = 0; t < NS; t++) qs[t] = NS == 1 || rs == t ? qop : (v4i){0, 0, 0, 0};
 
     AttnRows st;
-    st.m = live ? INT32_MIN : INT32_MAX;  // rows past the group's heads: never a record
+    st.m = live ? INT32_MIN : INT32_MAX;  // dead rows: never a record
     st.S = 0;
     for (int r = 0; r < 16; r++) st.vacc[r] = 0;
     if (a.sink) {  // attention.rs:211-224: sink score is the initial max, weight E(0) = 65535
@@ -104,63 +119,112 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p) {
     }
 
     const int ntiles = p / 64 + 1;  // keys 0..p; tile t0 + 64 <= p stays inside TP
-    // operands of tile t0 in one register set while the next tile's are loaded
-    // into the other; the last tile reloads itself, so the loads stay
-    // unconditional and nothing waits on them before their use
-    // (buffer loads: one 32-bit offset per lane, range-checked against the
-    // stream's TP * 64 bytes)
-    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)Kg, (short)0, a.TP * 64, BUF_DWORD3);
-    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)Vg, (short)0, a.TP * 64, BUF_DWORD3);
-    auto load_k = [&](v4i* k, int blk, int t) {
-        k[blk] = __builtin_amdgcn_raw_buffer_load_b128(rk, (t + blk * 16 + row) * 64 + grp * 16, 0, 0);
-    };
-    auto load_v = [&](v4i* v, int t) {
+    // buffer loads: one 32-bit offset per lane, range-checked against the
+    // stream's TP * 64 bytes of K ([TP][64]) and of V^T ([TP/16][64][16])
+    __amdgpu_buffer_rsrc_t rk[NS], rv[NS];
 #pragma unroll
-        for (int db = 0; db < 4; db++)
-            v[db] = __builtin_amdgcn_raw_buffer_load_b128(rv, ((t / 16 + grp) * 64 + db * 16 + row) * 16, 0, 0);
-    };
-    auto tile = [&](v4i* kc, v4i* vc, v4i* kn, v4i* vn, int t0) {
-        const int tn = t0 + 64 <= p ? t0 + 64 : t0;
-        int nvalid = p - (t0 + grp * 16) + 1;
-        nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
-        attn_tile<GEN>(
-            [&](int blk) {
-                load_k(kn, blk, tn);
-                return kc[blk];
-            },
-            [&](int db) { return vc[db]; }, qop, mscale, nvalid, t0 + 63 > p, nrows, lut32, wl[wave], st);
-        load_v(vn, tn);
-    };
-    v4i k0[4], v0[4], k1[4], v1[4];
-#pragma unroll
-    for (int blk = 0; blk < 4; blk++) load_k(k0, blk, 0);
-    load_v(v0, 0);
-    int kt = 0;
-    for (; kt + 1 < ntiles; kt += 2) {
-        tile(k0, v0, k1, v1, kt * 64);
-        tile(k1, v1, k0, v0, kt * 64 + 64);
+    for (int t = 0; t < NS; t++) {
+        const size_t base = ((size_t)bs[t] * a.KH + g) * a.TP * 64;
+        rk[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(a.kc + base), (short)0, a.TP * 64, BUF_DWORD3);
+        rv[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(a.vc + base), (short)0, a.TP * 64, BUF_DWORD3);
     }
-    if (kt < ntiles) tile(k0, v0, k1, v1, kt * 64);
+    auto load_k = [&](int t, int blk, int t0) {
+        return __builtin_amdgcn_raw_buffer_load_b128(rk[t], (t0 + blk * 16 + row) * 64 + grp * 16, 0, 0);
+    };
+    auto load_v = [&](int t, int db, int t0) {
+        return __builtin_amdgcn_raw_buffer_load_b128(rv[t], ((t0 / 16 + grp) * 64 + db * 16 + row) * 16, 0, 0);
+    };
+    auto nvalid_at = [&](int t0) {
+        const int n = p - (t0 + grp * 16) + 1;
+        return n < 0 ? 0 : (n > 16 ? 16 : n);
+    };
+    if constexpr (NS == 1) {
+        // two register sets: the tile's operands in one while the next tile's
+        // are loaded into the other; the last tile reloads itself, so the loads
+        // stay unconditional and nothing waits on them before their use
+        auto tile = [&](v4i* kc, v4i* vc, v4i* kn, v4i* vn, int t0) {
+            const int tn = t0 + 64 <= p ? t0 + 64 : t0;
+            attn_tile<GEN, 1>(
+                [&](int, int blk) {
+                    kn[blk] = load_k(0, blk, tn);
+                    return kc[blk];
+                },
+                [&](int, int db) { return vc[db]; }, [] {}, qs, 0, G, mscale, nvalid_at(t0), t0 + 63 > p, G, lut32,
+                wl[wave], st);
+#pragma unroll
+            for (int db = 0; db < 4; db++) vn[db] = load_v(0, db, tn);
+        };
+        v4i k0[4], v0[4], k1[4], v1[4];
+#pragma unroll
+        for (int blk = 0; blk < 4; blk++) k0[blk] = load_k(0, blk, 0);
+#pragma unroll
+        for (int db = 0; db < 4; db++) v0[db] = load_v(0, db, 0);
+        int kt = 0;
+        for (; kt + 1 < ntiles; kt += 2) {
+            tile(k0, v0, k1, v1, kt * 64);
+            tile(k1, v1, k0, v0, kt * 64 + 64);
+        }
+        if (kt < ntiles) tile(k0, v0, k1, v1, kt * 64);
+    } else {
+        // (all K loads before all V loads, as in the loop, so that the scores
+        // wait for the K operands only)
+        v4i kr[NS][4], vr[NS][4];
+#pragma unroll
+        for (int t = 0; t < NS; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) kr[t][i] = load_k(t, i, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < NS; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) vr[t][i] = load_v(t, i, 0);
+        for (int kt = 0; kt < ntiles; kt++) {
+            const int t0 = kt * 64;
+            const int tn = t0 + 64 <= p ? t0 + 64 : t0;
+            attn_tile<GEN, NS>(
+                [&](int t, int blk) { return kr[t][blk]; }, [&](int t, int db) { return vr[t][db]; },
+                [&] {
+#pragma unroll
+                    for (int t = 0; t < NS; t++)
+#pragma unroll
+                        for (int blk = 0; blk < 4; blk++) kr[t][blk] = load_k(t, blk, tn);
+                },
+                qs, rs, G, mscale, nvalid_at(t0), t0 + 63 > p, NS * G, lut32, wl[wave], st);
+#pragma unroll
+            for (int t = 0; t < NS; t++)
+#pragma unroll
+                for (int db = 0; db < 4; db++) vr[t][db] = load_v(t, db, tn);
+        }
+    }
     // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const unsigned Sr = (unsigned)__shfl((int)st.S, r, 64);
-        if (r < nrows) {
+        const int t = NS == 1 ? 0 : r / G;
+        if (r < NS * G && act[t < NS ? t : 0]) {
             const unsigned long long den = Sr == 0u ? 1ull : (unsigned long long)Sr;
-            a.out[(size_t)b * D + (h0 + r) * 64 + lane] = (int8_t)clamp127(div_rne_s32_u64((int)st.vacc[r], den));
+            a.out[(size_t)bs[t] * D + (h0 + r - t * G) * 64 + lane] =
+                (int8_t)clamp127(div_rne_s32_u64((int)st.vacc[r], den));
         }
     }
 }
 
 void launch_attn_decode(const AttnArgs& a, int S, int p, hipStream_t s) {
-    // a.H <= 16 (d_model <= 1024): every KV group fits one wavefront's rows
+    // heads per KV group: all of them in rust-compat mode (one KV head), H / G
+    // in GQA mode (n_heads is a multiple of n_kv_heads); at most 16
+    const int G = a.kv_mode == 1 ? a.H / a.G : a.H;
     AttnArgs g = a;
     g.B = S;
-    dim3 grid((unsigned)(((long long)S * a.KH + 3) / 4));
-    if (a.general)
-        hipLaunchKernelGGL(k_attn_decode<true>, grid, dim3(256), 0, s, g, p);
-    else
-        hipLaunchKernelGGL(k_attn_decode<false>, grid, dim3(256), 0, s, g, p);
+    const bool two = 2 * G <= 16;
+    const long long waves = (long long)(two ? (S + 1) / 2 : S) * a.KH;
+    dim3 grid((unsigned)((waves + 3) / 4));
+    if (two) {
+        if (a.general) hipLaunchKernelGGL((k_attn_decode<true, 2>), grid, dim3(256), 0, s, g, p, G);
+        else hipLaunchKernelGGL((k_attn_decode<false, 2>), grid, dim3(256), 0, s, g, p, G);
+    } else {
+        if (a.general) hipLaunchKernelGGL((k_attn_decode<true, 1>), grid, dim3(256), 0, s, g, p, G);
+        else hipLaunchKernelGGL((k_attn_decode<false, 1>), grid, dim3(256), 0, s, g, p, G);
+    }
 }
 
 // ---------------------------------------------------------------------------
