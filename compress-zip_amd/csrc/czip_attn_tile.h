@@ -103,7 +103,8 @@ struct AttnRows {
 // One 64-key tile.  kop(s, blk): the K operand of keys 16*blk + lane%16,
 // head dims 16*(lane/16) .. +16; vop(s, db): the V^T operand of head dim
 // 16*db + lane%16, keys 16*(lane/16) .. +16 (each called once per index);
-// after_scores() runs once the score products have consumed every K operand.
+// after_scan() runs once the scores have been scanned, before the V operands
+// are read.
 // nvalid: keys [16*(lane/16), +nvalid) of the lane's row are visible (the
 // others get weight 0 and are never records), used when diag is set; rows
 // >= nrows are not combined into vacc (their m, S and vacc are unused).
@@ -116,7 +117,7 @@ struct AttnRows {
 // own stream's keys and values: the streams are consecutive slices of the
 // contraction.  NS == 1: qs[0] is the query operand, rs and G are unused.
 template <bool GEN, int NS, class KOp, class VOp, class After>
-__device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scores, const v4i* qs, int rs, int G,
+__device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan, const v4i* qs, int rs, int G,
                                           double mscale, int nvalid, bool diag, int nrows, const unsigned* lut32,
                                           AttnWaveLds& W, AttnRows& st) {
     const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
@@ -130,7 +131,6 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_score
         *(int4*)&W.buf[row][blk * 16 + grp * 4] = make_int4(score_b<GEN>(sc[0], mscale), score_b<GEN>(sc[1], mscale),
                                                             score_b<GEN>(sc[2], mscale), score_b<GEN>(sc[3], mscale));
     }
-    after_scores();
     wave_lds_fence();
 
     // 2. in-order scan of keys [16*grp, 16*grp+16) of this row
@@ -237,6 +237,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_score
     }
 
     // 3. segment j of every row in pass j (MFMA column = row): O_j^T = V^T P_j^T
+    after_scan();
     if (grp == 0) W.nrec[row] = nrow;
     int nmax = nrow;
 #pragma unroll

@@ -59,8 +59,8 @@ void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s) 
 // streams share a wavefront (rows [0, G) and [G, 2G)), each meeting only its
 // own stream's keys.  Each lane loads its own K and V^T operand fragments
 // (16 bytes each) straight from the caches, one tile ahead: one stream into
-// a second register set, two streams in place (K once the scores have used
-// it, V after the tile's passes).
+// a second register set, two streams in place (the next K once the scores
+// are scanned, the next V after the tile's passes).
 // ---------------------------------------------------------------------------
 template <bool GEN, int NS>
 __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a, int p, int G) {
