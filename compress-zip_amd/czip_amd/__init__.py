@@ -22,6 +22,8 @@ from .build import LIB_PATH
 
 KV_RUST_COMPAT = 0
 KV_GQA = 1
+CODEC_ZSTD = 0     # outer codecs of the .czip container (file_format.rs:45-51)
+CODEC_BROTLI = 1
 BOS = 1022  # rust/src/main.rs:222
 
 STATUS = {
@@ -60,6 +62,15 @@ class ModelDesc(C.Structure):
     ]
 
 
+class ContainerInfo(C.Structure):
+    """czip_container: the header fields of a .czip file (file_format.rs:77-83, 158-165)."""
+    _fields_ = [
+        ("flags", C.c_uint8), ("codec", C.c_uint8), ("uncompressed_len", C.c_uint32),
+        ("model_id_hash", C.c_uint32), ("chunk_count", C.c_uint32), ("last_chunk_tokens", C.c_uint16),
+        ("tokenizer_id", C.c_uint8), ("context_length_log2", C.c_uint8),
+    ]
+
+
 # Functions declared in include/czip_hip.h, with their ctypes signatures.
 _P = C.c_void_p
 SIGNATURES = {
@@ -88,6 +99,12 @@ SIGNATURES = {
     "czip_tokenize": (C.c_int32, [_P, C.c_char_p, C.c_size_t, C.c_int32, _P, C.c_size_t,
                                   C.POINTER(C.c_size_t)]),
     "czip_detokenize": (C.c_int32, [_P, _P, C.c_size_t, _P, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "czip_model_id_hash": (C.c_uint32, [C.c_char_p, C.c_size_t]),
+    "czip_container_pack": (C.c_int32, [C.POINTER(ContainerInfo), _P, _P, C.POINTER(C.c_void_p),
+                                        C.POINTER(C.c_size_t)]),
+    "czip_container_unpack": (C.c_int32, [C.c_char_p, C.c_size_t, C.POINTER(ContainerInfo),
+                                          C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)]),
+    "czip_buffer_free": (None, [_P]),
     "czip_set_profiling": (None, [_P, C.c_int32]),
     "czip_kernel_stats": (C.c_int32, [_P, C.c_char_p, C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
     "czip_reset_stats": (None, [_P]),
@@ -333,3 +350,83 @@ class DecodeJob(Job):
         out = np.zeros(max(self.total_tokens, 1), np.uint32)
         self.model._check(lib().czip_decompress_fetch(self.h, _p(out), None))
         return out[:self.total_tokens]
+
+
+# ---------------------------------------------------------------------------
+# The .czip container and the whole-file flow of the reference CLI
+# (main.rs:125-302 compress, 304-399 decompress).
+# ---------------------------------------------------------------------------
+def level_to_context_length(level: int) -> int:
+    """main.rs:113-122: levels 1-5 are 64..1024 tokens per chunk, others 64."""
+    return {1: 64, 2: 128, 3: 256, 4: 512, 5: 1024}.get(level, 64)
+
+
+def model_id_hash(path: str) -> int:
+    """main.rs:79-85: the first 8 hex digits of MD5 of the model path as given."""
+    b = os.fsencode(path)
+    return int(lib().czip_model_id_hash(b, len(b)))
+
+
+def pack_czip(chunks, *, model_id_hash: int, context_length_log2: int, last_chunk_tokens: int,
+              uncompressed_len: int, codec: int = CODEC_BROTLI, tokenizer_id: int = 0, flags: int = 0) -> bytes:
+    """The .czip bytes of coded chunks (file_format.rs:385-392 + main.rs:255-279)."""
+    offs = np.zeros(len(chunks) + 1, np.int64)
+    offs[1:] = np.cumsum([len(c) for c in chunks]) if chunks else []
+    data = np.frombuffer(b"".join(chunks) or b"\0", np.uint8)
+    info = ContainerInfo(flags, codec, uncompressed_len, model_id_hash, len(chunks), last_chunk_tokens,
+                         tokenizer_id, context_length_log2)
+    out, n = C.c_void_p(), C.c_size_t()
+    rc = lib().czip_container_pack(C.byref(info), _p(data), _p(offs), C.byref(out), C.byref(n))
+    if rc:
+        raise CzipError(rc, "czip_container_pack")
+    try:
+        return C.string_at(out, n.value)
+    finally:
+        lib().czip_buffer_free(out)
+
+
+def unpack_czip(data: bytes):
+    """(header fields, list of chunk bytes) of a .czip file (main.rs:332-361)."""
+    info = ContainerInfo()
+    chunks, offs = C.c_void_p(), C.c_void_p()
+    rc = lib().czip_container_unpack(data, len(data), C.byref(info), C.byref(chunks), C.byref(offs))
+    if rc:
+        raise CzipError(rc, "czip_container_unpack")
+    try:
+        n = info.chunk_count
+        o = np.ctypeslib.as_array(C.cast(offs, C.POINTER(C.c_int64)), (n + 1,)).copy()
+        body = C.string_at(chunks, int(o[-1])) if o[-1] else b""
+    finally:
+        lib().czip_buffer_free(chunks)
+        lib().czip_buffer_free(offs)
+    fields = {f: getattr(info, f) for f, _ in ContainerInfo._fields_}
+    return fields, [body[o[i]:o[i + 1]] for i in range(n)]
+
+
+def chunk_token_counts(fields: dict):
+    """Tokens of each chunk (file_format.rs:333-352)."""
+    n = fields["chunk_count"]
+    per = 1 << fields["context_length_log2"]
+    return [per] * (n - 1) + [fields["last_chunk_tokens"]] if n else []
+
+
+def compress_text(model: "Model", tokenizer: "Tokenizer", text: bytes, model_path: str, level: int = None,
+                  codec: int = CODEC_BROTLI, threads: int = 16) -> bytes:
+    """main.rs:125-302: tokenize, code every chunk on the device, write the container.
+    level=None uses the model's context length, like the CLI without -L."""
+    cfg = model.weights.config
+    chunk = cfg["context_length"] if level is None else min(level_to_context_length(level), cfg["context_length"])
+    log2 = int(np.log2(chunk))
+    ids = tokenizer.encode(text, threads=threads)
+    chunks = model.compress_chunks(ids, chunk) if ids.size else []
+    last = ids.size - chunk * (len(chunks) - 1) if chunks else chunk
+    return pack_czip(chunks, model_id_hash=model_id_hash(model_path), context_length_log2=log2,
+                     last_chunk_tokens=last, uncompressed_len=len(text), codec=codec)
+
+
+def decompress_czip(model: "Model", tokenizer: "Tokenizer", data: bytes) -> bytes:
+    """main.rs:304-399: read the container, decode every chunk on the device, detokenize."""
+    fields, chunks = unpack_czip(data)
+    ntoks = chunk_token_counts(fields)
+    ids = model.decompress_chunks(chunks, ntoks) if chunks else np.zeros(0, np.uint32)
+    return tokenizer.decode_bytes(ids)

@@ -17,7 +17,7 @@ BUILD_DIR = os.path.join(ROOT, "_build")
 LIB_PATH = os.path.join(ROOT, "libczip_hip.so")
 
 SOURCES = ["czip_rows.hip", "czip_gemm.hip", "czip_head.hip", "czip_attention.hip", "czip_decode.hip", "czip_api.cpp",
-           "czm_loader.cpp", "czip_tokenizer.cpp"]
+           "czm_loader.cpp", "czip_tokenizer.cpp", "czip_container.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

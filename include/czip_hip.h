@@ -160,6 +160,42 @@ czip_status czip_tokenize(const czip_tokenizer* t, const char* text, size_t len,
 czip_status czip_detokenize(const czip_tokenizer* t, const uint32_t* ids, size_t n, uint8_t* out,
                             size_t cap, size_t* n_out);
 
+/* ---- CZIPv1 container (host): the .czip file of main.rs:241-279 / 339-361,
+ *      laid out by rust/src/file_format.rs.  A file is the 16-byte outer header
+ *      ("CZIPv1", flags, codec, uncompressed_len = input text bytes, header_len
+ *      = inner header bytes), then the outer codec's stream of the payload:
+ *      inner header (model_id_hash, chunk_count, last_chunk_tokens,
+ *      tokenizer_id, context_length_log2, one u16 byte length per chunk) and
+ *      the chunk bytes.  Codecs as main.rs: zstd level 22 or brotli quality 11,
+ *      window 22 (system libzstd / libbrotlienc / libbrotlidec).
+ *      czip_container_pack replaces CompressedFile::to_bytes_uncompressed plus
+ *      the codec (file_format.rs:385-392, main.rs:255-279): chunks holds the
+ *      chunk bytes back to back, chunk i at [offs[i], offs[i+1]) (chunk_count + 1
+ *      offsets); a chunk over 65535 bytes gives CZIP_E_OVERFLOW (file_format.rs:311).
+ *      czip_container_unpack replaces main.rs:332-361 + read_from_decompressed
+ *      (file_format.rs:355-382): malformed input gives CZIP_E_FORMAT; *chunks and
+ *      *offs are allocated by the library (release with czip_buffer_free).
+ *      czip_model_id_hash = hash_model_path (main.rs:79-85): the first 8 hex
+ *      digits of MD5(path). ---- */
+#define CZIP_CODEC_ZSTD   0
+#define CZIP_CODEC_BROTLI 1
+typedef struct czip_container {
+    uint8_t  flags;               /* bit 0: multifile (file_format.rs:69-73)  */
+    uint8_t  codec;               /* CZIP_CODEC_ZSTD or CZIP_CODEC_BROTLI      */
+    uint32_t uncompressed_len;    /* input text bytes                          */
+    uint32_t model_id_hash;
+    uint32_t chunk_count;
+    uint16_t last_chunk_tokens;
+    uint8_t  tokenizer_id;
+    uint8_t  context_length_log2; /* tokens per chunk = 1 << log2 (0 reads as 6) */
+} czip_container;
+uint32_t    czip_model_id_hash(const char* path, size_t len);
+czip_status czip_container_pack(const czip_container* info, const uint8_t* chunks, const int64_t* offs,
+                                uint8_t** out, size_t* out_len);
+czip_status czip_container_unpack(const uint8_t* data, size_t len, czip_container* info, uint8_t** chunks,
+                                  int64_t** offs);
+void        czip_buffer_free(void* p);
+
 /* ---- instrumentation: per-kernel HIP-event timing on the context stream. ---- */
 void        czip_set_profiling(czip_ctx* ctx, int32_t on);
 /* Kernel names: "prep","embed_norm","gemm_qkv","attention","gemm_o_norm",

@@ -345,6 +345,31 @@ def test_decompress_stream_groups(gpu_shipped, shipped, monkeypatch):
     assert np.array_equal(out, toks)
 
 
+@pytest.mark.parametrize("level", [1, 4])
+def test_czip_file_shipped(amd, orc, level):
+    """The CLI's whole flow (main.rs:125-399) on the shipped model: text ->
+    tokens -> device-coded chunks -> .czip (brotli) -> device decode -> text.
+    The container payload equals the one built from the oracle's chunk bytes
+    (file_format.rs layout restated in oracle/container.py)."""
+    import container as OC
+    from czip_amd import synth
+    w = amd.ModelWeights(MODEL_PATH)
+    gm = amd.Model(w)
+    tk = amd.Tokenizer(w)
+    text = synth.synthetic_text(24000 + 77 * level, seed=level)
+    _say(f"czip file level {level}")
+    data = amd.compress_text(gm, tk, text, "models/v001_eng.czm", level=level)
+    assert data[:6] == b"CZIPv1" and data[7] == amd.CODEC_BROTLI
+    chunk = amd.level_to_context_length(level)
+    ids = tk.encode(text)
+    ref_chunks = orc.Model.from_file(MODEL_PATH).compress_many(ids, chunk, threads=8)
+    last = ids.size - chunk * (len(ref_chunks) - 1)
+    exp = OC.payload(OC.model_id_hash("models/v001_eng.czm"), last, 0, chunk.bit_length() - 1, ref_chunks)
+    assert OC.decode_outer(amd.CODEC_BROTLI, data[16:]) == exp
+    assert data[:16] == OC.outer_header(0, amd.CODEC_BROTLI, len(text), 12 + 2 * len(ref_chunks))
+    assert amd.decompress_czip(gm, tk, data) == text
+
+
 def test_error_codes(gpu_shipped, amd):
     with pytest.raises(amd.CzipError) as e:
         gpu_shipped.compress_plan(np.zeros(10, np.uint32), 2048)   # past the 1024-entry RoPE LUT
