@@ -27,8 +27,9 @@ PEAK_HBM_GBS = 8000.0       # GB/s
 # HBM bytes per token (read + write) of each kernel on the text workload, from
 # two rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0: the factors a
 # plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text_1Mtok.md
-TRAFFIC_B_PER_TOKEN = {"attention": 994 + 396, "gemm_qkv": 1543 + 606, "gemm_o_norm": 401 + 1152,
-                       "gemm_down_norm": 1833 + 384, "gemm_up": 3072 + 1024, "head_cdf": 391 + 8}
+TRAFFIC_B_PER_TOKEN = {"attention": 514 + 384, "gemm_qkv": 389 + 513, "gemm_o_norm": 404 + 1152,
+                       "gemm_down_norm": 1816 + 384, "gemm_up": 390 + 1025, "head_cdf": 391 + 8,
+                       "embed_norm": 10 + 384}
 TRAFFIC_WORKLOADS = ("v001_L4_ctx512_text64MiB",)
 
 WORKLOADS = {
@@ -210,6 +211,17 @@ def main():
                 dk[name] = {"ms": round(tot, 3), "launches": launches}
         dec = {"value": round(n / (t1 - t0), 1), "unit": "tok/s", "ms": round((t1 - t0) * 1000, 2),
                "streams": len(chunks), "roundtrip_exact": True, "kernels": dk}
+        if "attn_decode" in dk:
+            # decode attention is HBM-bound: per stream-step, the cached K and V
+            # of every key so far (128 B per key and KV head) + q in + out
+            KH = cfg["n_kv_heads"] if kv_mode == czip_amd.KV_GQA else 1
+            D = cfg["n_heads"] * 64
+            keys = sum(t * (t + 1) // 2 for t in ntoks)
+            alg = cfg["n_layers"] * (keys * KH * 128 + n * 2 * D)
+            gbs = alg / (dk["attn_decode"]["ms"] / 1000.0) / 1e9
+            dec["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                               "frac": round(gbs / PEAK_HBM_GBS, 4), "kernel": "attn_decode",
+                               "algorithmic_bytes": alg}
 
     cpu = None
     if not args.no_cpu:
