@@ -37,6 +37,16 @@ WORKLOADS = {
     "v001_L4_ctx512_text64MiB": dict(model="shipped", chunk=512, text_bytes=64 << 20),
     # shipped model, level 4, Zipf(1.1) token ids (no tokenizer step)
     "v001_L4_ctx512_zipf16M": dict(model="shipped", chunk=512, ids=16 << 20),
+    # random-init d512 / 8 layers / 8 heads, 2 KV heads / F 2048 / V 1024, level 5
+    # (1024-token chunks), 16M Zipf ids, in the reference's KV semantics and in GQA
+    "d512L8_L5_ctx1024_zipf16M": dict(model="d512_l8", chunk=1024, ids=16 << 20, kv="rust_compat"),
+    "d512L8_L5_ctx1024_zipf16M_gqa": dict(model="d512_l8", chunk=1024, ids=16 << 20, kv="gqa"),
+    # the same model decoding 4096 concurrent streams of 512 tokens (its compress
+    # leg codes them at level 4)
+    "d512L8_decode_4096x512": dict(model="d512_l8", chunk=512, ids=4096 * 512, kv="rust_compat"),
+    # random-init d768 / 12 layers / 12 heads, 4 KV heads / F 3072 / V 8192, one
+    # 4096-token context per chunk, 8M Zipf ids; GQA only (attention.rs:172 rejects 12 heads)
+    "d768L12_ctx4096_zipf8M_gqa": dict(model="d768_l12", chunk=4096, ids=8 << 20, kv="gqa"),
 }
 DEFAULT = "v001_L4_ctx512_text64MiB"
 
@@ -71,7 +81,7 @@ def gemm_ops_per_token(cfg, kv_mode):
     return out
 
 
-def cpu_baseline(model_path, tokens, chunk, budget_s=15.0):
+def cpu_baseline(model_path, tokens, chunk, budget_s=15.0, kv_mode=0):
     """Oracle (C restatement of the Rust chunk loop) on the host cores."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
@@ -82,7 +92,7 @@ def cpu_baseline(model_path, tokens, chunk, budget_s=15.0):
         lib_path = oracle.LIB_PATH
         kind_note = "gcc -O3 -march=x86-64-v3"
     L = oracle.load(lib_path)
-    m = oracle.Model.from_file(model_path, lib_handle=L)
+    m = oracle.Model.from_file(model_path, kv_mode, lib_handle=L)
     cores = min(16, len(os.sched_getaffinity(0)))
     nchunks = len(tokens) // chunk
     # calibrate with one chunk per thread, then size the sample to the budget
@@ -121,8 +131,18 @@ def main():
         from czip_amd import build as b
         b.build()
     wl = WORKLOADS[args.workload]
-    model_path = os.path.join(ROOT, "models", "v001_eng.czm")
-    kv_mode = czip_amd.KV_RUST_COMPAT
+    if wl["model"] == "shipped":
+        model_path = os.path.join(ROOT, "models", "v001_eng.czm")
+        model_name = "v001_eng.czm"
+    else:
+        # random-init weights of the named shape (seeded), written once per run
+        import tempfile
+        from czip_amd import synth
+        model_path = os.path.join(tempfile.mkdtemp(prefix="czip_bench_"), wl["model"] + ".czm")
+        synth.write_random_model(model_path, seed=2024, **synth.MODEL_SHAPES[wl["model"]])
+        model_name = f"random-init {wl['model']} (seed 2024)"
+    kv_name = wl.get("kv", "rust_compat")
+    kv_mode = czip_amd.KV_GQA if kv_name == "gqa" else czip_amd.KV_RUST_COMPAT
     weights = czip_amd.ModelWeights(model_path, kv_mode)
     cfg = weights.config
     tokens, text, tokenizer = make_tokens(wl, weights, cfg["vocab_size"])
@@ -226,15 +246,16 @@ def main():
     cpu = None
     if not args.no_cpu:
         log("cpu baseline ...")
-        cpu = cpu_baseline(model_path, tokens, chunk, args.cpu_budget)
+        cpu = cpu_baseline(model_path, tokens, chunk, args.cpu_budget, kv_mode)
     line = {
-        "metric": "compress tok/s (bit-exact .czip payload) at L4 ctx512, 1 GPU",
+        "metric": ("compress tok/s (bit-exact .czip payload) at L4 ctx512, 1 GPU" if args.workload == DEFAULT
+                   else f"compress tok/s (bit-exact .czip payload), {args.workload}, 1 GPU"),
         "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8", "data": "synthetic",
-        "config": {"workload": args.workload, "model": "v001_eng.czm", "chunk_tokens": chunk, "tokens": n,
+        "config": {"workload": args.workload, "model": model_name, "chunk_tokens": chunk, "tokens": n,
                    "text_bytes": len(text) if text is not None else None,
-                   "chunks": len(chunks), "kv_mode": "rust_compat", "parallelism": "chunks"},
+                   "chunks": len(chunks), "kv_mode": kv_name, "parallelism": "chunks"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "decompress": dec,
