@@ -345,6 +345,38 @@ def test_decompress_stream_groups(gpu_shipped, shipped, monkeypatch):
     assert np.array_equal(out, toks)
 
 
+@pytest.mark.parametrize("kv", ["compat", "gqa"])
+def test_config_d512_l8_full_shape(amd, orc, tmp_path, kv):
+    """The d512 / 8-layer / 8 heads, 2 KV heads / F 2048 / V 1024 configuration
+    at its level-5 chunk size (1024 tokens): chunk bytes against the oracle
+    (one full chunk + a ragged one), then decoded on the device as concurrent
+    streams (the 4096-stream decode configuration at a test's size)."""
+    from czip_amd import synth
+    path = synth.write_random_model(str(tmp_path / "d512l8.czm"), seed=31, **synth.MODEL_SHAPES["d512_l8"])
+    mode = amd.KV_RUST_COMPAT if kv == "compat" else amd.KV_GQA
+    gm, om = _model_pair(amd, orc, path, mode)
+    n = 1024 + (333 if kv == "compat" else 96)
+    toks = synth.zipf_ids(n, 1024, seed=32)
+    _say(f"d512/L8 chunk 1024 {kv}: {n} tokens")
+    got = gm.compress_chunks(toks, 1024)
+    assert got == om.compress_many(toks, 1024, threads=8)
+    assert np.array_equal(gm.decompress_chunks(got, [1024, n - 1024]), toks)
+
+
+def test_config_d768_l12_full_shape(amd, orc, tmp_path):
+    """The d768 / 12-layer / 12 heads, 4 KV heads / F 3072 / V 8192 / 4096-context
+    configuration (GQA; the reference rejects 12 heads): a 384-token chunk of a
+    4096-token context, coded on the device against the oracle, and decoded."""
+    from czip_amd import synth
+    path = synth.write_random_model(str(tmp_path / "d768l12.czm"), seed=41, **synth.MODEL_SHAPES["d768_l12"])
+    gm, om = _model_pair(amd, orc, path, amd.KV_GQA)
+    toks = synth.zipf_ids(384, 8192, seed=42)
+    _say("d768/L12/V8192 chunk 4096: 384 tokens")
+    got = gm.compress_chunks(toks, 4096)
+    assert got == om.compress_many(toks, 4096, threads=8)
+    assert np.array_equal(gm.decompress_chunks(got, [384]), toks)
+
+
 @pytest.mark.parametrize("level", [1, 4])
 def test_czip_file_shipped(amd, orc, level):
     """The CLI's whole flow (main.rs:125-399) on the shipped model: text ->
