@@ -32,7 +32,6 @@ namespace czip {
 
 constexpr unsigned WOFF = 32896;      // w - WOFF spans [-32896, 32639] = 256*[-128,127] + [-128,127]
 constexpr int RS = 68;                // row stride (words) of the per-wave buffer: 16-byte accesses of 16 rows hit 64 banks
-constexpr int BUF_DWORD3 = 0x00020000;  // word 3 of a raw buffer resource: 32-bit data format, no swizzle
 
 struct AttnWaveLds {
     unsigned buf[16][RS];    // scores [row][key]; then per pass: column sums [column][dim]

@@ -26,6 +26,68 @@ __device__ __forceinline__ int clamp127(int x) { return x < -127 ? -127 : (x > 1
 // 4 extra cycles per read and 8 per store).
 __device__ __forceinline__ int lds64(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
 
+constexpr int BUF_DWORD3 = 0x00020000;  // word 3 of a raw buffer resource: 32-bit data format, no swizzle
+
+// acc[i][t] += A[m0 + 16 i + l%16, :] . W[nb + 16 t + l%16, :] over K (a
+// multiple of 64) for a workgroup that owns 64 rows of A: the 64 x 64 A tile
+// of each K step goes through double-buffered LDS (threads 0..255 stage 16
+// bytes each; rows past M read as 0 by the buffer range check), and each wave
+// streams its own CT W tiles straight into registers, in two register sets so
+// that the next step's loads are in flight while the current one multiplies.
+// W is the first MFMA operand: lane l ends with columns nb + 16 t + 4 (l / 16)
+// .. +3 of rows m0 + 16 i + l % 16.
+template <int CT>
+__device__ __forceinline__ void rowblock_mma(const int8_t* A, int M, int K, const int8_t* W, int wrows, int m0,
+                                             int nb, int8_t (*As)[64 * 64], v4i (&acc)[4][CT]) {
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15;
+    const int nk = K / 64;
+    const int arows = M - m0 < 64 ? M - m0 : 64;
+    const __amdgpu_buffer_rsrc_t rA =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(A + (size_t)m0 * K), (short)0, arows * K, BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, wrows * K, BUF_DWORD3);
+    const int aoff = (tid >> 2) * K + (tid & 3) * 16;
+    const int woff = (nb + lr) * K + (lane >> 4) * 16;
+    v4i ra = (v4i){0, 0, 0, 0};
+    auto fetch_a = [&](int k0) {
+        if (tid < 256) ra = __builtin_amdgcn_raw_buffer_load_b128(rA, aoff, k0, 0);
+    };
+    auto store_a = [&](int buf) {
+        if (tid < 256) *(v4i*)(As[buf] + lds64(tid >> 2, tid & 3)) = ra;
+    };
+    auto fetch_w = [&](v4i* w, int k0) {
+#pragma unroll
+        for (int t = 0; t < CT; t++) w[t] = __builtin_amdgcn_raw_buffer_load_b128(rW, woff + t * 16 * K, k0, 0);
+    };
+    auto step = [&](int kt, const v4i* wc, v4i* wn) {
+        const bool more = kt + 1 < nk;
+        if (more) {
+            fetch_a((kt + 1) * 64);
+            fetch_w(wn, (kt + 1) * 64);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the next step's loads ahead of this step's MFMAs
+        v4i af[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[kt & 1] + lds64(i * 16 + lr, lane >> 4));
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int t = 0; t < CT; t++) acc[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wc[t], af[i], acc[i][t], 0, 0, 0);
+        if (more) store_a((kt & 1) ^ 1);
+        __syncthreads();
+    };
+    v4i w0[CT], w1[CT];
+    fetch_a(0);
+    fetch_w(w0, 0);
+    store_a(0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        step(kt, w0, w1);
+        step(kt + 1, w1, w0);
+    }
+    if (kt < nk) step(kt, w0, w1);
+}
+
 // rint(a * b) (round half to even) for |a * b| < 2^31, exact when a * b is
 // exact in f64: adding 1.5 * 2^52 makes the ulp 1, so the FMA's single
 // rounding lands on the integer, and the low word of the sum is that integer

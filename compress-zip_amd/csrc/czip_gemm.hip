@@ -22,7 +22,6 @@ struct TileRegs {
     v4i v[2];
 };
 
-constexpr int BUF_DWORD3 = 0x00020000;  // word 3 of a raw buffer resource: 32-bit data format, no swizzle
 
 // The rows [row0, row0 + 128) of a row-major [rows_total, ld] int8 matrix as a
 // buffer resource: rows past rows_total read as 0 (range check).
@@ -88,7 +87,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     store_tile(ta, As[0], tid);
     store_tile(tw, Ws[0], tid);
     __syncthreads();
-    const int lr = lane & 15, lk = (lane >> 4) * 16;
+    const int lr = lane & 15;
     for (int kt = 0; kt < nk; kt++) {
         const int cur = kt & 1;
         if (kt + 1 < nk) {  // the next K step, fetched while this one is multiplied
@@ -268,8 +267,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int m0 = blockIdx.x * RBM;
     const int nb = wave * CT * 16;  // first output column of this wave
-    const int lr = lane & 15, lk = (lane >> 4) * 16, c4 = (lane >> 4) * 4;
-    const int nk = a.K / BK;
+    const int lr = lane & 15, c4 = (lane >> 4) * 4;
 
     v4i acc[4][CT];
 #pragma unroll
@@ -277,44 +275,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
 #pragma unroll
         for (int t = 0; t < CT; t++) acc[i][t] = (v4i){0, 0, 0, 0};
 
-    // A tile of a K step: 64 rows x 64 bytes, 16 bytes per thread of the first 256
-    const int ar = tid >> 2, ac = (tid & 3) * 16;
-    int4 ra = make_int4(0, 0, 0, 0);
-    auto fetch_a = [&](int k0) {
-        ra = make_int4(0, 0, 0, 0);
-        if (tid < 256 && m0 + ar < a.M) ra = *(const int4*)(a.A + (size_t)(m0 + ar) * a.K + k0 + ac);
-    };
-    auto store_a = [&](int buf) {
-        if (tid < 256) *(int4*)(As[buf] + lds64(ar, tid & 3)) = ra;
-    };
-    v4i wf[CT];
-    auto fetch_w = [&](int k0) {
-#pragma unroll
-        for (int t = 0; t < CT; t++) wf[t] = *(const v4i*)(a.W + (size_t)(nb + t * 16 + lr) * a.K + k0 + lk);
-    };
-    fetch_a(0);
-    fetch_w(0);
-    store_a(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        v4i wc[CT];
-#pragma unroll
-        for (int t = 0; t < CT; t++) wc[t] = wf[t];
-        if (kt + 1 < nk) {
-            fetch_a((kt + 1) * BK);
-            fetch_w((kt + 1) * BK);
-        }
-        v4i af[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[cur] + lds64(i * 16 + lr, lane >> 4));
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int t = 0; t < CT; t++) acc[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wc[t], af[i], acc[i][t], 0, 0, 0);
-        if (kt + 1 < nk) store_a(cur ^ 1);
-        __syncthreads();
-    }
+    rowblock_mma<CT>(a.A, a.M, a.K, a.W, a.d, m0, nb, As, acc);
 
     // epilogue.  Lane holds columns nb + 16 t + c4 .. +3 of rows m0 + 16 i + lr.
     // Its global operands (norm weights of its columns, residual input of its

@@ -19,7 +19,7 @@ namespace czip {
 // Lane l holds logits of rows 16 i + l % 16 (i < 4) at columns
 // 16 t + 4 (l / 16) .. +3 of its wave's range (t < CT).
 // ---------------------------------------------------------------------------
-constexpr int HBM_ROWS = 64, HBK = 64, HNW = 16;
+constexpr int HBM_ROWS = 64, HNW = 16;
 
 template <int CT>
 __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
@@ -34,8 +34,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int m0 = blockIdx.x * HBM_ROWS;
     const int nb = wave * CT * 16;
-    const int lr = lane & 15, lk = (lane >> 4) * 16, c4 = (lane >> 4) * 4;
-    const int nk = a.K / HBK;
+    const int lr = lane & 15, c4 = (lane >> 4) * 4;
     if (tid < 256) lut32[tid] = (unsigned)a.lut[tid] << 16;
 
     v4i acc[4][CT];
@@ -43,43 +42,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int t = 0; t < CT; t++) acc[i][t] = (v4i){0, 0, 0, 0};
-    const int ar = tid >> 2, ac = (tid & 3) * 16;
-    int4 ra = make_int4(0, 0, 0, 0);
-    auto fetch_a = [&](int k0) {
-        ra = make_int4(0, 0, 0, 0);
-        if (tid < 256 && m0 + ar < a.M) ra = *(const int4*)(a.A + (size_t)(m0 + ar) * a.K + k0 + ac);
-    };
-    auto store_a = [&](int buf) {
-        if (tid < 256) *(int4*)(As[buf] + lds64(ar, tid & 3)) = ra;
-    };
-    v4i wf[CT];
-    auto fetch_w = [&](int k0) {
-#pragma unroll
-        for (int t = 0; t < CT; t++) wf[t] = *(const v4i*)(a.W + (size_t)(nb + t * 16 + lr) * a.K + k0 + lk);
-    };
-    fetch_a(0);
-    fetch_w(0);
-    store_a(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        v4i wc[CT];
-#pragma unroll
-        for (int t = 0; t < CT; t++) wc[t] = wf[t];
-        if (kt + 1 < nk) {
-            fetch_a((kt + 1) * HBK);
-            fetch_w((kt + 1) * HBK);
-        }
-        v4i af[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[cur] + lds64(i * 16 + lr, lane >> 4));
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int t = 0; t < CT; t++) acc[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wc[t], af[i], acc[i][t], 0, 0, 0);
-        if (kt + 1 < nk) store_a(cur ^ 1);
-        __syncthreads();
-    }
+    rowblock_mma<CT>(a.A, a.M, a.K, a.W, a.V, m0, nb, As, acc);
 
     // targets of the lane's rows, requested before the reductions
     int tokr[4];
