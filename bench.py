@@ -225,7 +225,7 @@ def main():
             raise SystemExit("detokenized output differs from the input text")
         dk = {}
         for name in ["dec_init", "dec_prep", "embed_norm", "gemm_qkv", "attn_decode", "gemm_o", "gemm_o_norm",
-                     "row_norm", "gemm_up", "gemm_down", "gemm_down_norm", "gemm_head", "cdf_decode"]:
+                     "row_norm", "gemm_up", "gemm_down", "gemm_down_norm", "head_dec", "gemm_head", "cdf_decode"]:
             launches, tot = model.kernel_stats(name)
             if launches:
                 dk[name] = {"ms": round(tot, 3), "launches": launches}

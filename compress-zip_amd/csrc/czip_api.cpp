@@ -72,7 +72,7 @@ struct czip_ctx {
     czip_model_desc cfg{};
     int KH = 1;  // cached KV heads per layer
     bool rn_fused = false;  // residual + norms fused into the row GEMM (gemm_rn_supported(d_model))
-    bool head_fused = false;  // compress: LM head fused with the coder interval stage (head_cdf_supported(vocab))
+    bool head_fused = false;  // LM head fused with the coder interval stage / decode step (head_cdf_supported(vocab))
     std::vector<void*> allocs;
     int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr;
     uint16_t* lut = nullptr;
@@ -729,7 +729,7 @@ extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t* data, co
     const size_t d = (size_t)c->cfg.d_model, L = (size_t)c->cfg.n_layers;
     double gb = 16.0;
     if (const char* s = getenv("CZIP_SCRATCH_GB")) gb = atof(s);
-    const double per_stream = (double)row_bytes(c) + 2.0 * L * (double)c->KH * pad64(Tcap) * 64 + 64;
+    const double per_stream = (double)row_bytes(c, !c->head_fused) + 2.0 * L * (double)c->KH * pad64(Tcap) * 64 + 64;
     int64_t S = (int64_t)(gb * 1e9 / per_stream);
     if (const char* s = getenv("CZIP_DECODE_STREAMS")) S = std::min<int64_t>(S, atoll(s));
     S = std::max<int64_t>(1, std::min<int64_t>(S, std::max(nchunks, 1)));
@@ -749,7 +749,7 @@ extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t* data, co
         (rc = dalloc(c, A, &j->x, (size_t)S * d)) || (rc = dalloc(c, A, &j->xn, (size_t)S * d)) ||
         (rc = dalloc(c, A, &j->q8, (size_t)S * d)) || (rc = dalloc(c, A, &j->attn, (size_t)S * d)) ||
         (rc = dalloc(c, A, &j->y8, (size_t)S * d)) || (rc = dalloc(c, A, &j->r8, (size_t)S * c->cfg.d_ff)) ||
-        (rc = dalloc(c, A, &j->logits, (size_t)S * c->cfg.vocab)) ||
+        (rc = dalloc(c, A, &j->logits, c->head_fused ? 1 : (size_t)S * c->cfg.vocab)) ||
         (rc = dalloc(c, A, &j->kc, L * (size_t)S * c->KH * pad64(Tcap) * 64)) ||
         (rc = dalloc(c, A, &j->vc, L * (size_t)S * c->KH * pad64(Tcap) * 64))) {
         free_job_mem(j.get());
@@ -806,10 +806,18 @@ static czip_status run_decompress(czip_job* j) {
                 { Timed t(c, "attn_decode"); launch_attn_decode(a, S, p, s); }
                 post_attention(c, j, l, S);
             }
-            GemmArgs hd{};
-            hd.A = j->xn; hd.W = c->head_w; hd.M = S; hd.N = V; hd.K = d; hd.out32 = j->logits; hd.ldo = V;
-            { Timed t(c, "gemm_head"); launch_gemm(hd, EPI_RAW, s); }
-            { Timed t(c, "cdf_decode"); launch_cdf_decode(j->logits, S, V, c->lut, c->cfg.coef_q24, c->cfg.target_total, p, st, ds, s); }
+            if (c->head_fused) {
+                HeadDecArgs h{};
+                h.A = j->xn; h.W = c->head_w; h.M = S; h.K = d; h.V = V;
+                h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total; h.p = p;
+                Timed t(c, "head_dec");
+                launch_head_dec(h, st, ds, s);
+            } else {
+                GemmArgs hd{};
+                hd.A = j->xn; hd.W = c->head_w; hd.M = S; hd.N = V; hd.K = d; hd.out32 = j->logits; hd.ldo = V;
+                { Timed t(c, "gemm_head"); launch_gemm(hd, EPI_RAW, s); }
+                { Timed t(c, "cdf_decode"); launch_cdf_decode(j->logits, S, V, c->lut, c->cfg.coef_q24, c->cfg.target_total, p, st, ds, s); }
+            }
         }
     }
     HIPCHECK(c, hipGetLastError());

@@ -2,6 +2,7 @@
 // step, each stream a chunk of the .czip payload (main.rs:377-396), with an
 // arithmetic decoder per stream kept on the device (arith_coder.rs:139-264).
 #include "czip_attn_tile.h"
+#include "czip_head.h"
 #include "czip_kernels.h"
 
 namespace czip {
@@ -395,6 +396,164 @@ void launch_cdf_decode(const int32_t* logits, int S, int V, const uint16_t* lut,
     else
         hipLaunchKernelGGL((k_cdf_decode<4, 32>), dim3((unsigned)S), dim3(256), 0, s, logits, V, lut, coef, total, p,
                            st, ds);
+}
+
+// ---------------------------------------------------------------------------
+// One decode step with the logits kept on chip: a workgroup owns 64 streams
+// (the rows of head_freqs).  After the frequency table, per row:
+//   - wave 0 (lane = row) forms the remainder total - sum f, the exclusive
+//     prefix of the 16 wave ranges (the argmax's wave carrying the
+//     remainder) and value = ((code - low + 1) * total - 1) / range, clamped
+//     to total - 1 (a value >= total decodes as the last symbol, whose
+//     interval ends at total: arith_coder.rs:225-241);
+//   - every lane scans its columns in column order (tile, lane group, element)
+//     from its wave's base, the lane-group prefix within a tile by two
+//     shuffles; the one column with lo <= value < hi is the symbol;
+//   - wave 0 narrows the interval and renormalizes (arith_coder.rs:243-262)
+//     reading bits from an 8-byte window of the stream (a step shifts at most
+//     32 bits: each pass shifts a 0 into low and a 1 into high, and after 32
+//     of them low = 0, high = 2^32 - 1 ends the loop).
+// ---------------------------------------------------------------------------
+template <int CT>
+__global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState st, DecStreams ds) {
+    __shared__ HeadLds L;
+    __shared__ unsigned row_v[HBM_ROWS], row_rem[HBM_ROWS], row_lo[HBM_ROWS], row_hi[HBM_ROWS];
+    __shared__ int row_sym[HBM_ROWS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int m0 = blockIdx.x * HBM_ROWS;
+    const int nb = wave * CT * 16;
+    const int lr = lane & 15, grp = lane >> 4, c4 = grp * 4;
+    // decoder state of wave 0's stream, requested before the GEMM
+    const int b = m0 + lane;
+    bool live = false;
+    unsigned low = 0, high = 0, code = 0;
+    if (wave == 0 && b < a.M && a.p < ds.ntok[b]) {
+        live = true;
+        low = st.low[b];
+        high = st.high[b];
+        code = st.code[b];
+    }
+    v4i acc[4][CT];
+    head_freqs<CT>(a.A, a.M, a.K, a.W, a.V, m0, a.lut, a.coef, a.total, L, acc);
+    // sum f per row and wave
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        unsigned fs = 0;
+#pragma unroll
+        for (int t = 0; t < CT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) fs += (unsigned)acc[i][t][r];
+        fs += (unsigned)__shfl_xor((int)fs, 16, 64);
+        fs += (unsigned)__shfl_xor((int)fs, 32, 64);
+        if (lane < 16) L.red_b[wave][i * 16 + lane] = fs;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        unsigned tot = 0;
+#pragma unroll
+        for (int w = 0; w < HNW; w++) tot += L.red_b[w][lane];
+        const unsigned rem = a.total - tot;
+        const int wam = L.row_am[lane] / (CT * 16);
+        unsigned run = 0;
+#pragma unroll
+        for (int w = 0; w < HNW; w++) {
+            L.red_c[w][lane] = run;
+            run += L.red_b[w][lane] + (w == wam ? rem : 0u);
+        }
+        const unsigned long long range = (unsigned long long)high - low + 1;  // <= 2^32
+        const unsigned long long value = ((unsigned long long)(code - low) + 1) * a.total - 1;
+        row_v[lane] = live ? (unsigned)min(value / range, (unsigned long long)a.total - 1) : 0u;
+        row_rem[lane] = rem;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int rr = i * 16 + lr;
+        const unsigned v = row_v[rr], rem = row_rem[rr];
+        const int am = L.row_am[rr];
+        unsigned run = L.red_c[wave][rr];
+#pragma unroll
+        for (int t = 0; t < CT; t++) {
+            unsigned g = 0;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int col = nb + t * 16 + c4 + r;
+                const unsigned f = (unsigned)acc[i][t][r] + (col == am ? rem : 0u);
+                acc[i][t][r] = (int)f;
+                g += f;
+            }
+            // inclusive prefix over the four lane groups of the row, and their total
+            unsigned x = g;
+            const unsigned y1 = (unsigned)__shfl_up((int)x, 16, 64);
+            x += grp >= 1 ? y1 : 0u;
+            const unsigned y2 = (unsigned)__shfl_up((int)x, 32, 64);
+            x += grp >= 2 ? y2 : 0u;
+            const unsigned tile_sum = (unsigned)__shfl((int)x, lr + 48, 64);
+            unsigned lo = run + x - g;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const unsigned hi = lo + (unsigned)acc[i][t][r];
+                if (lo <= v && v < hi) {
+                    row_sym[rr] = nb + t * 16 + c4 + r;
+                    row_lo[rr] = lo;
+                    row_hi[rr] = hi;
+                }
+                lo = hi;
+            }
+            run += tile_sum;
+        }
+    }
+    __syncthreads();
+    if (!live) return;
+    const unsigned long long range = (unsigned long long)high - low + 1;
+    const double invT = 1.0 / (double)a.total;
+    unsigned long long nh = low + udiv64_32((unsigned long long)row_hi[lane] * range, a.total, invT) - 1;
+    unsigned long long nl = low + udiv64_32((unsigned long long)row_lo[lane] * range, a.total, invT);
+    unsigned long long cd = code;
+    // bits MSB first from byte bp, bit bi on (zeros past the end: arith_coder.rs:176-190)
+    const uint8_t* data = ds.data + ds.offs[b];
+    const long long len = ds.blen[b];
+    const long long bp = st.byte_pos[b];
+    const int bi = st.bit_pos[b];
+    unsigned long long win = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) win |= (unsigned long long)(bp + k < len ? data[bp + k] : 0) << (56 - 8 * k);
+    int pos = 56 + bi;  // window bit of the next stream bit
+    for (;;) {
+        if (((nl ^ nh) & DHALF) == 0) {
+            nl = (nl << 1) & DMASK;
+            nh = ((nh << 1) & DMASK) | 1;
+            cd = ((cd << 1) & DMASK) | ((win >> pos) & 1);
+            pos--;
+        } else if ((nl & ~nh & DQUART) != 0) {
+            nl = ((nl << 1) ^ DHALF) & DMASK;
+            nh = (((nh ^ DHALF) << 1) | DHALF | 1) & DMASK;
+            cd = (cd & DHALF) | ((cd << 1) & (DMASK >> 1)) | ((win >> pos) & 1);
+            pos--;
+        } else {
+            break;
+        }
+    }
+    // reader position after the bits taken (it stops at the end of the chunk)
+    const long long used = (long long)(7 - bi) + (56 + bi - pos);
+    long long nbp = bp + used / 8;
+    int nbi = 7 - (int)(used % 8);
+    if (bp >= len) { nbp = bp; nbi = bi; }
+    else if (nbp >= len) { nbp = len; nbi = 7; }
+    st.low[b] = (uint32_t)nl;
+    st.high[b] = (uint32_t)nh;
+    st.code[b] = (uint32_t)cd;
+    st.byte_pos[b] = nbp;
+    st.bit_pos[b] = nbi;
+    ds.tokens[ds.tok_offs[b] + a.p] = (uint32_t)row_sym[lane];
+}
+
+void launch_head_dec(const HeadDecArgs& a, DecState st, DecStreams ds, hipStream_t s) {
+    dim3 grid((unsigned)((a.M + HBM_ROWS - 1) / HBM_ROWS));
+    switch (a.V) {
+        case 512: hipLaunchKernelGGL(k_head_dec<2>, grid, dim3(64 * HNW), 0, s, a, st, ds); break;
+        default: hipLaunchKernelGGL(k_head_dec<4>, grid, dim3(64 * HNW), 0, s, a, st, ds); break;
+    }
 }
 
 }  // namespace czip

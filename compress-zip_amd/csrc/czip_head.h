@@ -1,0 +1,129 @@
+// The LM head and the frequency table of a block of 64 rows, shared by the
+// compress interval stage (czip_head.hip) and the decode step (czip_decode.hip):
+// model.rs:470-477 + softmax_cdf.rs:85-139 with the int32 logits kept on chip.
+#pragma once
+
+#include "czip_device.h"
+
+namespace czip {
+
+// A workgroup owns 64 token rows and all V logits of each (16 waves, wave w
+// holds columns [w*V/16, (w+1)*V/16) as CT = V/256 MFMA tiles of 16).  Lane l
+// holds rows 16 i + l % 16 (i < 4) at columns 16 t + 4 (l / 16) .. +3 of its
+// wave's range (t < CT).
+constexpr int HBM_ROWS = 64, HNW = 16;
+
+struct HeadLds {
+    int8_t As[2][HBM_ROWS * 64] __attribute__((aligned(16)));
+    unsigned lut32[256];
+    int red_a[HNW][HBM_ROWS];
+    unsigned red_b[HNW][HBM_ROWS], red_c[HNW][HBM_ROWS];
+    int row_i[HBM_ROWS], row_am[HBM_ROWS];
+    unsigned row_Q[HBM_ROWS];
+    double row_Rm[HBM_ROWS], row_inv[HBM_ROWS];
+};
+
+// Logits of the block (rowblock_mma), then per row, with two block reductions:
+//   1. max logit;
+//   2. first argmax (row_am) and S = sum E(l - max) (softmax_cdf.rs:96-110);
+// and every element's frequency f = 1 + e*Q + floor(e*Rm / S) (Q = R / S,
+// Rm = R % S, R = total - V) in place of its logit.  floor(e*Rm/S) is
+// floor(fma(e*Rm, 1/S, 2^-30)) in f64: e*Rm < 2^42 is exact, a nonzero
+// fraction of e*Rm/S is >= 1/S >= 2^-26, and the f64 error of the product
+// with the rounded 1/S is < 2^-35 for quotients below 2^16.  The argmax's
+// remainder (total - sum f) is left to the caller.
+template <int CT>
+__device__ __forceinline__ void head_freqs(const int8_t* A, int M, int K, const int8_t* W, int V, int m0,
+                                           const uint16_t* lut, unsigned coef, unsigned total, HeadLds& L,
+                                           v4i (&acc)[4][CT]) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int nb = wave * CT * 16;
+    const int lr = lane & 15, c4 = (lane >> 4) * 4;
+    if (tid < 256) L.lut32[tid] = (unsigned)lut[tid] << 16;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int t = 0; t < CT; t++) acc[i][t] = (v4i){0, 0, 0, 0};
+    rowblock_mma<CT>(A, M, K, W, V, m0, nb, L.As, acc);
+
+    // 1. row max
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int mx = INT32_MIN;
+#pragma unroll
+        for (int t = 0; t < CT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) mx = max(mx, acc[i][t][r]);
+        mx = max(mx, __shfl_xor(mx, 16, 64));
+        mx = max(mx, __shfl_xor(mx, 32, 64));
+        if (lane < 16) L.red_a[wave][i * 16 + lane] = mx;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int mx = L.red_a[0][lane];
+#pragma unroll
+        for (int w = 1; w < HNW; w++) mx = max(mx, L.red_a[w][lane]);
+        L.row_i[lane] = mx;
+    }
+    __syncthreads();
+    // 2. first argmax and S = sum of e = E(l - max)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int mx = L.row_i[i * 16 + lr];
+        int am = 0x7FFFFFFF;
+        unsigned s = 0;
+#pragma unroll
+        for (int t = 0; t < CT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int col = nb + t * 16 + c4 + r;
+                const int l = acc[i][t][r];
+                am = (l == mx && col < am) ? col : am;
+                const unsigned e = exp_q16_bf((int)((unsigned)l - (unsigned)mx), L.lut32, coef);
+                acc[i][t][r] = (int)e;
+                s += e;
+            }
+        am = min(am, __shfl_xor(am, 16, 64));
+        am = min(am, __shfl_xor(am, 32, 64));
+        s += (unsigned)__shfl_xor((int)s, 16, 64);
+        s += (unsigned)__shfl_xor((int)s, 32, 64);
+        if (lane < 16) {
+            L.red_a[wave][i * 16 + lane] = am;
+            L.red_b[wave][i * 16 + lane] = s;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int am = L.red_a[0][lane];
+        unsigned S = L.red_b[0][lane];
+#pragma unroll
+        for (int w = 1; w < HNW; w++) {
+            am = min(am, L.red_a[w][lane]);
+            S += L.red_b[w][lane];
+        }
+        const unsigned R = total - (unsigned)V;  // S <= 1024 * 65535 < 2^26
+        const unsigned Q = R / S;
+        L.row_am[lane] = am;
+        L.row_Q[lane] = Q;
+        L.row_Rm[lane] = (double)(R - Q * S);
+        L.row_inv[lane] = 1.0 / (double)S;
+    }
+    __syncthreads();
+    // f in place of e
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int rr = i * 16 + lr;
+        const unsigned Q = L.row_Q[rr];
+        const double Rm = L.row_Rm[rr], inv = L.row_inv[rr];
+#pragma unroll
+        for (int t = 0; t < CT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const unsigned e = (unsigned)acc[i][t][r];
+                const unsigned q = (unsigned)__builtin_fma((double)e * Rm, inv, 0x1p-30);
+                acc[i][t][r] = (int)(1u + __umul24(e, Q) + q);  // e < 2^16, Q < 2^15
+            }
+    }
+}
+
+}  // namespace czip

@@ -130,5 +130,16 @@ void launch_attn_decode(const AttnArgs& a, int S, int p, hipStream_t s);
 // logits -> cumulative frequencies -> one arithmetic-decode step (arith_coder.rs:195-264)
 void launch_cdf_decode(const int32_t* logits, int S, int V, const uint16_t* lut, unsigned coef, unsigned total,
                        int p, DecState st, DecStreams ds, hipStream_t s);
+// LM head + frequency table + symbol search + decoder step of S streams in one
+// kernel (head_cdf_supported(V)); A = the final-normalized rows [S, K]
+struct HeadDecArgs {
+    const int8_t* A;
+    const int8_t* W;           // [V, K]
+    int M, K, V;
+    const uint16_t* lut;       // [256]
+    unsigned coef, total;
+    int p;                     // step
+};
+void launch_head_dec(const HeadDecArgs& a, DecState st, DecStreams ds, hipStream_t s);
 
 }  // namespace czip

@@ -201,7 +201,8 @@ void        czip_set_profiling(czip_ctx* ctx, int32_t on);
 /* Kernel names: "prep","embed_norm","gemm_qkv","attention","gemm_o_norm",
  * "gemm_up","gemm_down_norm","head_cdf","encode"; where a fused kernel has no
  * instance for the model shape: "gemm_o","gemm_down","row_norm","gemm_head",
- * "cdf"; decode: "dec_init","dec_prep","attn_decode","cdf_decode". */
+ * "cdf"; decode: "dec_init","dec_prep","attn_decode","head_dec" (or, unfused,
+ * "gemm_head","cdf_decode"). */
 czip_status czip_kernel_stats(czip_ctx* ctx, const char* name, int64_t* launches, double* total_ms);
 void        czip_reset_stats(czip_ctx* ctx);
 
