@@ -1,4 +1,7 @@
 // int8 MFMA GEMMs with fused epilogues (linear.rs:12-31 + model.rs:280-300).
+#include <algorithm>
+#include <cstdlib>
+
 #include "czip_device.h"
 #include "czip_kernels.h"
 
@@ -58,6 +61,112 @@ __device__ __forceinline__ unsigned pack4i(int a, int b, int c, int d) {
     return (unsigned)(a & 0xFF) | ((unsigned)(b & 0xFF) << 8) | ((unsigned)(c & 0xFF) << 16) | ((unsigned)d << 24);
 }
 
+// Chunk, position and RoPE cos/sin (columns c4 .. c4+3 of each 16-wide half)
+// of one output row of the QKV projection.
+struct QkvRow {
+    int p, b;
+    unsigned cs[2][2], sn[2][2];
+};
+
+__device__ __forceinline__ void qkv_row(const GemmArgs& a, int row, int c4, QkvRow& q) {
+    row = min(row, a.M - 1);
+    int b = (int)((float)row * (1.0f / (float)a.T));  // row < 2^24: within one of row / T
+    if (b * a.T > row) b--;
+    else if ((b + 1) * a.T <= row) b++;
+    q.p = a.pos >= 0 ? a.pos : row - b * a.T;
+    q.b = a.pos >= 0 ? row : b;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint2 c = *(const uint2*)(a.rcos + q.p * 32 + j * 16 + c4);
+        const uint2 sv = *(const uint2*)(a.rsin + q.p * 32 + j * 16 + c4);
+        q.cs[j][0] = c.x; q.cs[j][1] = c.y;
+        q.sn[j][0] = sv.x; q.sn[j][1] = sv.y;
+    }
+}
+
+// Epilogue of one 16-row x 64-column tile: acc[j] holds columns
+// col_base + 16 j + c4 .. +3 of `row` (col_base 64-aligned: one head / one
+// gate-up group).  The caller checks row < M and col_base < N.
+template <int EPI, bool FAST>
+__device__ __forceinline__ void epi_tile(const GemmArgs& a, const v4i* acc, int row, int col_base, int c4,
+                                         const QkvRow& q) {
+    if (EPI == EPI_RAW) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *(int4*)(a.out32 + (size_t)row * a.ldo + col_base + j * 16 + c4) =
+                make_int4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+    } else if (EPI == EPI_REQ) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *(unsigned*)(a.out8 + (size_t)row * a.ldo + col_base + j * 16 + c4) =
+                pack4i(rq<FAST>(acc[j][0], a), rq<FAST>(acc[j][1], a), rq<FAST>(acc[j][2], a), rq<FAST>(acc[j][3], a));
+    } else if (EPI == EPI_REGLU) {
+        // W rows were permuted so that a 64-row group holds 32 gate rows then the
+        // matching 32 up rows: output feature f = col_base/2 + j*16 + c4 + r.
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            int o[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int g = rq<FAST>(acc[j][r], a);
+                const int u = rq<FAST>(acc[j + 2][r], a);
+                const int gr = g > 0 ? g : 0;
+                o[r] = clamp127(rne_shr(gr * u, 7));  // reglu.rs:20-46 (|gr * u| <= 127^2)
+            }
+            *(unsigned*)(a.out8 + (size_t)row * a.ldo + (col_base >> 1) + j * 16 + c4) = pack4i(o[0], o[1], o[2], o[3]);
+        }
+    } else {  // EPI_QKV
+        const int p = q.p, b = q.b;
+        const int kcol = col_base - a.d;
+        int g = 0, isv = 0;
+        if (kcol >= 0) {
+            if (a.kv_mode == 1) { isv = kcol >= 64 * a.G; g = (isv ? kcol - 64 * a.G : kcol) >> 6; }
+            else isv = kcol >= 64;
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int i0 = j * 16 + c4;  // rotary pairs (i0 + r, i0 + r + 32)
+            int xq[4], yq[4], xv[4], yv[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                xv[r] = rq<FAST>(acc[j][r], a);
+                yv[r] = rq<FAST>(acc[j + 2][r], a);
+                const int c = (int16_t)(r & 1 ? q.cs[j][r >> 1] >> 16 : q.cs[j][r >> 1] & 0xFFFFu);
+                const int sn = (int16_t)(r & 1 ? q.sn[j][r >> 1] >> 16 : q.sn[j][r >> 1] & 0xFFFFu);
+                const int xr = (int)((unsigned)(xv[r] * c) - (unsigned)(yv[r] * sn));
+                const int yr = (int)((unsigned)(xv[r] * sn) + (unsigned)(yv[r] * c));
+                if (kcol < 0) {
+                    // Q: attention.rs:53-83 (>>15 then NET_SHIFT=1, two roundings)
+                    xq[r] = clamp127(rne_shr(rne_shr(xr, 15), 1));
+                    yq[r] = clamp127(rne_shr(rne_shr(yr, 15), 1));
+                } else {
+                    // K: attention.rs:29-50 (|xr|, |yr| <= 2 * 127 * 32768)
+                    xq[r] = clamp127(rne_shr(xr, 15));
+                    yq[r] = clamp127(rne_shr(yr, 15));
+                }
+            }
+            if (kcol < 0) {
+                int8_t* qo = a.out8 + (size_t)row * a.ldo + col_base;
+                *(unsigned*)(qo + i0) = pack4i(xq[0], xq[1], xq[2], xq[3]);
+                *(unsigned*)(qo + i0 + 32) = pack4i(yq[0], yq[1], yq[2], yq[3]);
+            } else if (!isv) {
+                int8_t* k = a.kc + (((size_t)b * a.KH + g) * a.T + p) * 64;
+                *(unsigned*)(k + i0) = pack4i(xq[0], xq[1], xq[2], xq[3]);
+                *(unsigned*)(k + i0 + 32) = pack4i(yq[0], yq[1], yq[2], yq[3]);
+            } else {
+                // V^T in blocks of 16 keys, [key/16][dim][16]: the PV operand
+                // of both attention kernels is 16 consecutive keys of one dim
+                int8_t* v = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP + (size_t)(p >> 4) * 1024 + (p & 15);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    v[(i0 + r) * 16] = (int8_t)xv[r];
+                    v[(i0 + r + 32) * 16] = (int8_t)yv[r];
+                }
+            }
+        }
+    }
+}
+
 template <int EPI, bool FAST>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) int8_t As[2][BM * 64];
@@ -114,109 +223,102 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     const int col_base = n0 + wn * 64;  // 64-aligned, one head / one gate-up group
     if (col_base >= a.N) return;
     const int c4 = (lane >> 4) * 4;  // first of this lane's 4 consecutive columns in a 16-wide tile
-    // QKV: position and chunk of the lane's 4 rows, and their RoPE cos/sin for
-    // columns i0 .. i0+3 (8-byte loads, all issued before the arithmetic)
-    int rowpos[4], rowchunk[4];
-    unsigned cs[4][2][2], sn2[4][2][2];
+    // QKV: chunk, position and RoPE cos/sin of the lane's 4 rows, all loads
+    // issued before the arithmetic
+    QkvRow qr[4];
     if (EPI == EPI_QKV) {
-        const float invT = 1.0f / (float)a.T;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int row = min(m0 + wm * 64 + i * 16 + lr, a.M - 1);
-            int b = (int)((float)row * invT);  // row < 2^24: within one of row / T
-            if (b * a.T > row) b--;
-            else if ((b + 1) * a.T <= row) b++;
-            rowpos[i] = a.pos >= 0 ? a.pos : row - b * a.T;
-            rowchunk[i] = a.pos >= 0 ? row : b;
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const uint2 c = *(const uint2*)(a.rcos + rowpos[i] * 32 + j * 16 + c4);
-                const uint2 sv = *(const uint2*)(a.rsin + rowpos[i] * 32 + j * 16 + c4);
-                cs[i][j][0] = c.x; cs[i][j][1] = c.y;
-                sn2[i][j][0] = sv.x; sn2[i][j][1] = sv.y;
-            }
-        }
+        for (int i = 0; i < 4; i++) qkv_row(a, m0 + wm * 64 + i * 16 + lr, c4, qr[i]);
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int row = m0 + wm * 64 + i * 16 + lr;
         if (row >= a.M) continue;
-        if (EPI == EPI_RAW) {
+        epi_tile<EPI, FAST>(a, acc[i], row, col_base, c4, qr[i]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent W-stationary GEMM for K = 64 KS (KS <= 8): each wave keeps its 64
+// columns of W for the whole K in registers (4 x KS MFMA operands, loaded
+// once), a workgroup of 4 waves owns 256 columns, and the rows of A stream
+// through in strips of 64: the next strip is fetched into registers while the
+// current one, double-buffered in LDS as KS 64 x 64 tiles, is multiplied, one
+// 16-row tile at a time with its epilogue straight after.  Only A crosses LDS
+// (64 B of LDS reads per 16 K MACs per lane), and no W byte is re-read.
+// Workgroups are dispatched round-robin over the 8 XCDs: the ncg column groups
+// of one row worker sit on one XCD and walk the same strips, so each strip is
+// fetched from HBM by one L2.
+// ---------------------------------------------------------------------------
+constexpr int WS_SR = 64;
+
+template <int EPI, bool FAST, int KS>
+__global__ __launch_bounds__(256, 2) void k_gemm_ws(GemmArgs a, int ncg) {
+    __shared__ __attribute__((aligned(16))) int8_t As[2][KS * WS_SR * 64];
+    constexpr int K = KS * 64;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, c4 = (lane >> 4) * 4;
+    const int xcd = (int)(blockIdx.x % NXCD), jx = (int)(blockIdx.x / NXCD);
+    const int cg = jx % ncg;
+    const int worker = (jx / ncg) * NXCD + xcd, nworkers = (int)gridDim.x / ncg;
+    const int nstrips = (a.M + WS_SR - 1) / WS_SR;
+    if (worker >= nstrips) return;  // the whole workgroup
+    const int col_base = cg * 256 + wave * 64;
+    const bool wlive = col_base < a.N;
+
+    // this wave's W: w[j][ks] = rows col_base + 16 j + lane % 16, bytes 64 ks + 16 (lane / 16) .. +16
+    v4i w[4][KS];
+    {
+        const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.N * K, BUF_DWORD3);
+        const int woff = (col_base + lr) * K + (lane >> 4) * 16;
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                *(int4*)(a.out32 + (size_t)row * a.ldo + col_base + j * 16 + c4) =
-                    make_int4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
-        } else if (EPI == EPI_REQ) {
+        for (int j = 0; j < 4; j++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                *(unsigned*)(a.out8 + (size_t)row * a.ldo + col_base + j * 16 + c4) =
-                    pack4i(rq<FAST>(acc[i][j][0], a), rq<FAST>(acc[i][j][1], a), rq<FAST>(acc[i][j][2], a),
-                           rq<FAST>(acc[i][j][3], a));
-        } else if (EPI == EPI_REGLU) {
-            // W rows were permuted so that a 64-row group holds 32 gate rows then the
-            // matching 32 up rows: output feature f = col_base/2 + j*16 + c4 + r.
+            for (int ks = 0; ks < KS; ks++) w[j][ks] = __builtin_amdgcn_raw_buffer_load_b128(rW, woff + j * 16 * K, ks * 64, 0);
+    }
+    // strip staging: thread -> row tid / 4, 16-byte chunk tid % 4 of each 64-byte K step
+    const int srow = tid >> 2, sch = tid & 3;
+    v4i st[KS];
+    auto fetch = [&](int s) {
+        const int r0 = s * WS_SR;
+        const int rows = min(a.M - r0, WS_SR);
+        const __amdgpu_buffer_rsrc_t rA =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(a.A + (size_t)r0 * K), (short)0, rows * K, BUF_DWORD3);
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                int o[4];
+        for (int ks = 0; ks < KS; ks++) st[ks] = __builtin_amdgcn_raw_buffer_load_b128(rA, srow * K + sch * 16, ks * 64, 0);
+    };
+    auto store = [&](int buf) {
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int g = rq<FAST>(acc[i][j][r], a);
-                    const int u = rq<FAST>(acc[i][j + 2][r], a);
-                    const int gr = g > 0 ? g : 0;
-                    o[r] = clamp127(rne_shr(gr * u, 7));  // reglu.rs:20-46 (|gr * u| <= 127^2)
+        for (int ks = 0; ks < KS; ks++) *(v4i*)(As[buf] + ks * WS_SR * 64 + lds64(srow, sch)) = st[ks];
+    };
+    fetch(worker);
+    store(0);
+    __syncthreads();
+    int cur = 0;
+    for (int s = worker; s < nstrips; s += nworkers) {
+        const bool more = s + nworkers < nstrips;
+        if (more) fetch(s + nworkers);
+        if (wlive) {
+            QkvRow qr[2];
+            if (EPI == EPI_QKV) qkv_row(a, s * WS_SR + lr, c4, qr[0]);
+#pragma unroll
+            for (int i = 0; i < WS_SR / 16; i++) {
+                v4i acc[4];
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    const v4i af = *(const v4i*)(As[cur] + ks * WS_SR * 64 + lds64(i * 16 + lr, lane >> 4));
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j][ks], af, ks == 0 ? (v4i){0, 0, 0, 0} : acc[j],
+                                                                       0, 0, 0);
                 }
-                *(unsigned*)(a.out8 + (size_t)row * a.ldo + (col_base >> 1) + j * 16 + c4) = pack4i(o[0], o[1], o[2], o[3]);
-            }
-        } else {  // EPI_QKV
-            const int p = rowpos[i], b = rowchunk[i];
-            const int kcol = col_base - a.d;
-            int g = 0, isv = 0;
-            if (kcol >= 0) {
-                if (a.kv_mode == 1) { isv = kcol >= 64 * a.G; g = (isv ? kcol - 64 * a.G : kcol) >> 6; }
-                else isv = kcol >= 64;
-            }
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int i0 = j * 16 + c4;  // rotary pairs (i0 + r, i0 + r + 32)
-                int xq[4], yq[4], xv[4], yv[4];
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    xv[r] = rq<FAST>(acc[i][j][r], a);
-                    yv[r] = rq<FAST>(acc[i][j + 2][r], a);
-                    const int c = (int16_t)(r & 1 ? cs[i][j][r >> 1] >> 16 : cs[i][j][r >> 1] & 0xFFFFu);
-                    const int sn = (int16_t)(r & 1 ? sn2[i][j][r >> 1] >> 16 : sn2[i][j][r >> 1] & 0xFFFFu);
-                    const int xr = (int)((unsigned)(xv[r] * c) - (unsigned)(yv[r] * sn));
-                    const int yr = (int)((unsigned)(xv[r] * sn) + (unsigned)(yv[r] * c));
-                    if (kcol < 0) {
-                        // Q: attention.rs:53-83 (>>15 then NET_SHIFT=1, two roundings)
-                        xq[r] = clamp127(rne_shr(rne_shr(xr, 15), 1));
-                        yq[r] = clamp127(rne_shr(rne_shr(yr, 15), 1));
-                    } else {
-                        // K: attention.rs:29-50 (|xr|, |yr| <= 2 * 127 * 32768)
-                        xq[r] = clamp127(rne_shr(xr, 15));
-                        yq[r] = clamp127(rne_shr(yr, 15));
-                    }
-                }
-                if (kcol < 0) {
-                    int8_t* q = a.out8 + (size_t)row * a.ldo + col_base;
-                    *(unsigned*)(q + i0) = pack4i(xq[0], xq[1], xq[2], xq[3]);
-                    *(unsigned*)(q + i0 + 32) = pack4i(yq[0], yq[1], yq[2], yq[3]);
-                } else if (!isv) {
-                    int8_t* k = a.kc + (((size_t)b * a.KH + g) * a.T + p) * 64;
-                    *(unsigned*)(k + i0) = pack4i(xq[0], xq[1], xq[2], xq[3]);
-                    *(unsigned*)(k + i0 + 32) = pack4i(yq[0], yq[1], yq[2], yq[3]);
-                } else {
-                    // V^T in blocks of 16 keys, [key/16][dim][16]: the PV operand
-                    // of both attention kernels is 16 consecutive keys of one dim
-                    int8_t* v = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP + (size_t)(p >> 4) * 1024 + (p & 15);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        v[(i0 + r) * 16] = (int8_t)xv[r];
-                        v[(i0 + r + 32) * 16] = (int8_t)yv[r];
-                    }
-                }
+                if (EPI == EPI_QKV && i + 1 < WS_SR / 16) qkv_row(a, s * WS_SR + (i + 1) * 16 + lr, c4, qr[(i + 1) & 1]);
+                const int row = s * WS_SR + i * 16 + lr;
+                if (row < a.M) epi_tile<EPI, FAST>(a, acc, row, col_base, c4, qr[i & 1]);
             }
         }
+        if (more) store(cur ^ 1);
+        __syncthreads();
+        cur ^= 1;
     }
 }
 
@@ -228,7 +330,39 @@ static void launch_epi(const GemmArgs& a, dim3 grid, hipStream_t s) {
         hipLaunchKernelGGL((k_gemm<EPI, false>), grid, dim3(256), 0, s, a);
 }
 
+template <int EPI, int KS>
+static void launch_ws(const GemmArgs& a, hipStream_t s) {
+    // two workgroups per CU (256 CUs), ncg column groups per row worker, the
+    // workers a multiple of the 8 XCDs and no more than the strips
+    const int ncg = (a.N + 255) / 256;
+    const int nstrips = (a.M + WS_SR - 1) / WS_SR;
+    int workers = std::max(NXCD, (512 / ncg) / NXCD * NXCD);
+    workers = std::min(workers, (nstrips + NXCD - 1) / NXCD * NXCD);
+    dim3 grid((unsigned)(workers * ncg));
+    if (a.rq_fast)
+        hipLaunchKernelGGL((k_gemm_ws<EPI, true, KS>), grid, dim3(256), 0, s, a, ncg);
+    else
+        hipLaunchKernelGGL((k_gemm_ws<EPI, false, KS>), grid, dim3(256), 0, s, a, ncg);
+}
+
+template <int EPI>
+static bool try_ws(const GemmArgs& a, hipStream_t s) {
+    static const bool off = getenv("CZIP_GEMM_TILED") != nullptr;
+    if (off || a.N % 64 != 0 || (long long)a.N * a.K >= (1ll << 31) || a.M <= 0) return false;
+    switch (a.K) {
+        case 384: launch_ws<EPI, 6>(a, s); return true;
+        case 512: launch_ws<EPI, 8>(a, s); return true;
+        default: return false;
+    }
+}
+
 void launch_gemm(const GemmArgs& a, int epi, hipStream_t s) {
+    switch (epi) {
+        case EPI_RAW: if (try_ws<EPI_RAW>(a, s)) return; break;
+        case EPI_REQ: if (try_ws<EPI_REQ>(a, s)) return; break;
+        case EPI_QKV: if (try_ws<EPI_QKV>(a, s)) return; break;
+        default: if (try_ws<EPI_REGLU>(a, s)) return; break;
+    }
     const int ntm = (a.M + BM - 1) / BM, ntn = (a.N + BN - 1) / BN;
     dim3 grid((unsigned)(((ntm + NXCD - 1) / NXCD) * NXCD * ntn));
     switch (epi) {
