@@ -12,6 +12,7 @@
 namespace czip {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 constexpr unsigned ATTN_COEF_Q24 = 378194u;  // (LOG2E / 64 * 2^24 + 0.5) as u32, attention.rs:17-19
 constexpr uint32_t BOS_TOKEN = 1022u;        // main.rs:222, 387

@@ -238,32 +238,209 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     }
 }
 
+// Output resources of one strip: rows past M (and, for the caches, rows whose
+// offset is forced out of range) are dropped by the buffer range check.
+struct WsOut {
+    __amdgpu_buffer_rsrc_t o;      // out8 / out32 from the strip's first row r0
+    __amdgpu_buffer_rsrc_t k, v;   // QKV: K / V^T caches from chunk b0
+    int r0, b0;
+};
+
+// The results of one 16 x 64 tile, packed for its stores: REQ / QKV Q and K
+// the row's 16 bytes at columns 16 (lane / 16) .., REGLU its 8 bytes at
+// 8 (lane / 16) .. of the 32 outputs, V the x / y bytes of the two rotary
+// groups (four to a dword); off = where they go (for the caches, out of range
+// for rows past M).
+struct WsTile {
+    unsigned d[4];
+    int off;
+};
+
+// 4 x 4 dword transpose over the four 16-lane groups: on entry group g holds
+// x[j] = X[g][j], on exit X[j][g] (gfx950 permlane swaps: 32 exchanges lane
+// halves, 16 the odd and even 16-lane rows).
+__device__ __forceinline__ void transpose4(unsigned (&x)[4]) {
+    auto a = __builtin_amdgcn_permlane32_swap(x[0], x[2], false, false);
+    auto b = __builtin_amdgcn_permlane32_swap(x[1], x[3], false, false);
+    auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    x[0] = c[0]; x[1] = c[1]; x[2] = d[0]; x[3] = d[1];
+}
+
+// 4 x 2: group g holds X[g][0], X[g][1]; on exit the 8 bytes of
+// (X[2h][j], X[2h + 1][j]) with j = g / 2, h = g % 2
+__device__ __forceinline__ void transpose2(unsigned& x0, unsigned& x1) {
+    auto a = __builtin_amdgcn_permlane32_swap(x0, x1, false, false);
+    auto c = __builtin_amdgcn_permlane16_swap(a[0], a[1], false, false);
+    x0 = c[0]; x1 = c[1];
+}
+
+// Epilogue arithmetic of one tile (as epi_tile).  ROLE of a QKV wave: 0 its 64
+// columns are a query head, 1 the key head g, 2 the value head g.  EPI_RAW
+// stores at once (16 dwords per tile are too many to hold).
+template <int EPI, bool FAST, int ROLE>
+__device__ __forceinline__ void epi_ws(const GemmArgs& a, const WsOut& ro, const v4i* acc, int row, int col_base,
+                                       int c4, const QkvRow& q, int g, WsTile& t) {
+    if (EPI == EPI_RAW) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            __builtin_amdgcn_raw_buffer_store_b128(acc[j], ro.o, ((row - ro.r0) * a.ldo + col_base + j * 16 + c4) * 4, 0, 0);
+    } else if (EPI == EPI_REQ) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            t.d[j] = pack4i(rq<FAST>(acc[j][0], a), rq<FAST>(acc[j][1], a), rq<FAST>(acc[j][2], a), rq<FAST>(acc[j][3], a));
+        transpose4(t.d);
+        t.off = (row - ro.r0) * a.ldo + col_base + c4 * 4;
+    } else if (EPI == EPI_REGLU) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            int o[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int gg = rq<FAST>(acc[j][r], a);
+                const int u = rq<FAST>(acc[j + 2][r], a);
+                const int gr = gg > 0 ? gg : 0;
+                o[r] = clamp127(rne_shr(gr * u, 7));  // reglu.rs:20-46
+            }
+            t.d[j] = pack4i(o[0], o[1], o[2], o[3]);
+        }
+        transpose2(t.d[0], t.d[1]);
+        t.off = (row - ro.r0) * a.ldo + (col_base >> 1) + c4 * 2;
+    } else {  // EPI_QKV
+        const bool valid = row < a.M;
+        const int p = q.p, bl = q.b - ro.b0;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            int xq[4], yq[4], xv[4], yv[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                xv[r] = rq<FAST>(acc[j][r], a);
+                yv[r] = rq<FAST>(acc[j + 2][r], a);
+                if (ROLE != 2) {
+                    const int c = (int16_t)(r & 1 ? q.cs[j][r >> 1] >> 16 : q.cs[j][r >> 1] & 0xFFFFu);
+                    const int sn = (int16_t)(r & 1 ? q.sn[j][r >> 1] >> 16 : q.sn[j][r >> 1] & 0xFFFFu);
+                    const int xr = (int)((unsigned)(xv[r] * c) - (unsigned)(yv[r] * sn));
+                    const int yr = (int)((unsigned)(xv[r] * sn) + (unsigned)(yv[r] * c));
+                    if (ROLE == 0) {  // attention.rs:53-83
+                        xq[r] = clamp127(rne_shr(rne_shr(xr, 15), 1));
+                        yq[r] = clamp127(rne_shr(rne_shr(yr, 15), 1));
+                    } else {  // attention.rs:29-50
+                        xq[r] = clamp127(rne_shr(xr, 15));
+                        yq[r] = clamp127(rne_shr(yr, 15));
+                    }
+                }
+            }
+            if (ROLE != 2) {  // 16-column tiles: x of group j is tile j, y tile 2 + j
+                t.d[j] = pack4i(xq[0], xq[1], xq[2], xq[3]);
+                t.d[2 + j] = pack4i(yq[0], yq[1], yq[2], yq[3]);
+            } else {
+                t.d[2 * j] = pack4i(xv[0], xv[1], xv[2], xv[3]);
+                t.d[2 * j + 1] = pack4i(yv[0], yv[1], yv[2], yv[3]);
+            }
+        }
+        if (ROLE != 2) transpose4(t.d);
+        if (ROLE == 0) t.off = (row - ro.r0) * a.ldo + col_base + c4 * 4;
+        else if (ROLE == 1) t.off = valid ? ((bl * a.KH + g) * a.T + p) * 64 + c4 * 4 : (int)0xFFFFFF00u;
+        else t.off = valid ? (bl * a.KH + g) * 64 * a.TP + (p >> 4) * 1024 + (p & 15) + c4 * 16 : (int)0xFFFF0000u;
+    }
+}
+
+// The stores of one tile.
+template <int EPI, int ROLE>
+__device__ __forceinline__ void flush_ws(const WsOut& ro, const WsTile& t) {
+    if (EPI == EPI_REQ || (EPI == EPI_QKV && ROLE != 2)) {
+        __builtin_amdgcn_raw_buffer_store_b128((v4i){(int)t.d[0], (int)t.d[1], (int)t.d[2], (int)t.d[3]},
+                                               EPI == EPI_QKV && ROLE == 1 ? ro.k : ro.o, t.off, 0, 0);
+    } else if (EPI == EPI_REGLU) {
+        __builtin_amdgcn_raw_buffer_store_b64((v2i){(int)t.d[0], (int)t.d[1]}, ro.o, t.off, 0, 0);
+    } else if (EPI == EPI_QKV) {
+        // V^T in blocks of 16 keys, [key/16][dim][16]: dim i is at byte 16 i
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                __builtin_amdgcn_raw_buffer_store_b8((unsigned char)(t.d[2 * j] >> (8 * r)), ro.v,
+                                                     t.off + (j * 16 + r) * 16, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b8((unsigned char)(t.d[2 * j + 1] >> (8 * r)), ro.v,
+                                                     t.off + (j * 16 + r + 32) * 16, 0, 0);
+            }
+    }
+}
+
+// The 16-row tiles of one SR-row strip for this wave's 64 columns, the
+// epilogue arithmetic of tile i between the MFMAs of tile i + 1; the results
+// stay in t for the stores.
+template <int EPI, bool FAST, int KS, int SR, int ROLE>
+__device__ __forceinline__ void ws_strip(const GemmArgs& a, const WsOut& ro, const v4i (&w)[4][KS],
+                                         const int8_t* As, int r0, int col_base, int g, WsTile (&t)[SR / 16]) {
+    const int lane = threadIdx.x & 63, lr = lane & 15, c4 = (lane >> 4) * 4;
+    auto mma = [&](int i, v4i* acc) {
+        v4i af[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) af[ks] = *(const v4i*)(As + ks * SR * 64 + lds64(i * 16 + lr, lane >> 4));
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j][ks], af[ks], ks == 0 ? (v4i){0, 0, 0, 0} : acc[j], 0, 0, 0);
+    };
+    QkvRow qr[2];
+    if (EPI == EPI_QKV) qkv_row(a, r0 + lr, c4, qr[0]);
+    v4i acc[2][4];
+    mma(0, acc[0]);
+#pragma unroll
+    for (int i = 0; i < SR / 16; i++) {
+        if (i + 1 < SR / 16) {
+            if (EPI == EPI_QKV) qkv_row(a, r0 + (i + 1) * 16 + lr, c4, qr[(i + 1) & 1]);
+            mma(i + 1, acc[(i + 1) & 1]);
+        }
+        epi_ws<EPI, FAST, ROLE>(a, ro, acc[i & 1], r0 + i * 16 + lr, col_base, c4, qr[i & 1], g, t[i]);
+    }
+}
+
+template <int EPI, int NT, int ROLE>
+__device__ __forceinline__ void ws_flush(const WsOut& ro, const WsTile (&t)[NT]) {
+#pragma unroll
+    for (int i = 0; i < NT; i++) flush_ws<EPI, ROLE>(ro, t[i]);
+}
+
 // ---------------------------------------------------------------------------
 // Persistent W-stationary GEMM for K = 64 KS (KS <= 8): each wave keeps its 64
 // columns of W for the whole K in registers (4 x KS MFMA operands, loaded
 // once), a workgroup of 4 waves owns 256 columns, and the rows of A stream
-// through in strips of 64: the next strip is fetched into registers while the
-// current one, double-buffered in LDS as KS 64 x 64 tiles, is multiplied, one
-// 16-row tile at a time with its epilogue straight after.  Only A crosses LDS
-// (64 B of LDS reads per 16 K MACs per lane), and no W byte is re-read.
-// Workgroups are dispatched round-robin over the 8 XCDs: the ncg column groups
-// of one row worker sit on one XCD and walk the same strips, so each strip is
-// fetched from HBM by one L2.
+// through in strips of SR (64; 32 for QKV, whose epilogue holds more): the
+// next strip is fetched into registers while the current one, double-buffered
+// in LDS as KS SR x 64 tiles, is multiplied, and the strip's outputs are
+// stored after the next strip is in LDS.
+// Only A crosses LDS (64 B of LDS reads per 16 K MACs per lane), and no W
+// byte is re-read.  Workgroups are dispatched round-robin over the 8 XCDs:
+// the ncg column groups of one row worker sit on one XCD and walk the same
+// strips, so each strip is fetched from HBM by one L2.
 // ---------------------------------------------------------------------------
-constexpr int WS_SR = 64;
-
-template <int EPI, bool FAST, int KS>
+template <int EPI, bool FAST, int KS, int SR>
 __global__ __launch_bounds__(256, 2) void k_gemm_ws(GemmArgs a, int ncg) {
-    __shared__ __attribute__((aligned(16))) int8_t As[2][KS * WS_SR * 64];
+    __shared__ __attribute__((aligned(16))) int8_t As[2][KS * SR * 64];
+    constexpr int NT = SR / 16, KPT = KS * SR / 64;  // tiles per strip, staging loads per thread
     constexpr int K = KS * 64;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, c4 = (lane >> 4) * 4;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15;
     const int xcd = (int)(blockIdx.x % NXCD), jx = (int)(blockIdx.x / NXCD);
     const int cg = jx % ncg;
     const int worker = (jx / ncg) * NXCD + xcd, nworkers = (int)gridDim.x / ncg;
-    const int nstrips = (a.M + WS_SR - 1) / WS_SR;
+    const int nstrips = (a.M + SR - 1) / SR;
     if (worker >= nstrips) return;  // the whole workgroup
     const int col_base = cg * 256 + wave * 64;
     const bool wlive = col_base < a.N;
+    // QKV: the wave's role and KV head
+    int role = 0, g = 0;
+    if (EPI == EPI_QKV) {
+        const int kcol = col_base - a.d;
+        if (kcol >= 0) {
+            int isv;
+            if (a.kv_mode == 1) { isv = kcol >= 64 * a.G; g = (isv ? kcol - 64 * a.G : kcol) >> 6; }
+            else isv = kcol >= 64;
+            role = isv ? 2 : 1;
+        }
+    }
 
     // this wave's W: w[j][ks] = rows col_base + 16 j + lane % 16, bytes 64 ks + 16 (lane / 16) .. +16
     v4i w[4][KS];
@@ -275,20 +452,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ws(GemmArgs a, int ncg) {
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) w[j][ks] = __builtin_amdgcn_raw_buffer_load_b128(rW, woff + j * 16 * K, ks * 64, 0);
     }
-    // strip staging: thread -> row tid / 4, 16-byte chunk tid % 4 of each 64-byte K step
-    const int srow = tid >> 2, sch = tid & 3;
-    v4i st[KS];
+    WsOut ro;
+    // strip staging: thread -> row (tid / 4) % SR, 16-byte chunk tid % 4 of the
+    // 64-byte K steps ks = kg, kg + 64 / SR, ... (kg = tid / (4 SR))
+    const int srow = (tid >> 2) % SR, sch = tid & 3, kg = (tid >> 2) / SR;
+    v4i st[KPT];
     auto fetch = [&](int s) {
-        const int r0 = s * WS_SR;
-        const int rows = min(a.M - r0, WS_SR);
+        const int r0 = s * SR;
+        const int rows = min(a.M - r0, SR);
         const __amdgpu_buffer_rsrc_t rA =
             __builtin_amdgcn_make_buffer_rsrc((void*)(a.A + (size_t)r0 * K), (short)0, rows * K, BUF_DWORD3);
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) st[ks] = __builtin_amdgcn_raw_buffer_load_b128(rA, srow * K + sch * 16, ks * 64, 0);
+        for (int n = 0; n < KPT; n++)
+            st[n] = __builtin_amdgcn_raw_buffer_load_b128(rA, srow * K + sch * 16, (kg + n * (64 / SR)) * 64, 0);
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) *(v4i*)(As[buf] + ks * WS_SR * 64 + lds64(srow, sch)) = st[ks];
+        for (int n = 0; n < KPT; n++) *(v4i*)(As[buf] + (kg + n * (64 / SR)) * SR * 64 + lds64(srow, sch)) = st[n];
     };
     fetch(worker);
     store(0);
@@ -297,26 +477,41 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ws(GemmArgs a, int ncg) {
     for (int s = worker; s < nstrips; s += nworkers) {
         const bool more = s + nworkers < nstrips;
         if (more) fetch(s + nworkers);
-        if (wlive) {
-            QkvRow qr[2];
-            if (EPI == EPI_QKV) qkv_row(a, s * WS_SR + lr, c4, qr[0]);
-#pragma unroll
-            for (int i = 0; i < WS_SR / 16; i++) {
-                v4i acc[4];
-#pragma unroll
-                for (int ks = 0; ks < KS; ks++) {
-                    const v4i af = *(const v4i*)(As[cur] + ks * WS_SR * 64 + lds64(i * 16 + lr, lane >> 4));
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j][ks], af, ks == 0 ? (v4i){0, 0, 0, 0} : acc[j],
-                                                                       0, 0, 0);
-                }
-                if (EPI == EPI_QKV && i + 1 < WS_SR / 16) qkv_row(a, s * WS_SR + (i + 1) * 16 + lr, c4, qr[(i + 1) & 1]);
-                const int row = s * WS_SR + i * 16 + lr;
-                if (row < a.M) epi_tile<EPI, FAST>(a, acc, row, col_base, c4, qr[i & 1]);
-            }
+        const int r0 = s * SR;
+        ro.r0 = r0;
+        {
+            const int ob = min(a.M - r0, SR) * a.ldo * (EPI == EPI_RAW ? 4 : 1);
+            if (EPI == EPI_RAW)
+                ro.o = __builtin_amdgcn_make_buffer_rsrc((void*)(a.out32 + (size_t)r0 * a.ldo), (short)0, ob, BUF_DWORD3);
+            else
+                ro.o = __builtin_amdgcn_make_buffer_rsrc((void*)(a.out8 + (size_t)r0 * a.ldo), (short)0, ob, BUF_DWORD3);
         }
+        if (EPI == EPI_QKV) {
+            // the caches from the strip's first chunk: every offset of the
+            // strip's rows fits 31 bits (SR rows, KH * T * 64 < 2^24 per chunk)
+            const long long nb = a.pos >= 0 ? a.M : (a.M + a.T - 1) / a.T;
+            ro.b0 = a.pos >= 0 ? r0 : r0 / a.T;
+            const long long kb = (long long)a.KH * a.T * 64, vb = (long long)a.KH * 64 * a.TP;
+            ro.k = __builtin_amdgcn_make_buffer_rsrc((void*)(a.kc + ro.b0 * kb), (short)0,
+                                                     (int)min((nb - ro.b0) * kb, 0x7FFFFFFFll), BUF_DWORD3);
+            ro.v = __builtin_amdgcn_make_buffer_rsrc((void*)(a.vc + ro.b0 * vb), (short)0,
+                                                     (int)min((nb - ro.b0) * vb, 0x7FFFFFFFll), BUF_DWORD3);
+        }
+        WsTile t[NT];
+        if (wlive) {
+            if (EPI != EPI_QKV || role == 0) ws_strip<EPI, FAST, KS, SR, 0>(a, ro, w, As[cur], r0, col_base, g, t);
+            else if (role == 1) ws_strip<EPI, FAST, KS, SR, 1>(a, ro, w, As[cur], r0, col_base, g, t);
+            else ws_strip<EPI, FAST, KS, SR, 2>(a, ro, w, As[cur], r0, col_base, g, t);
+        }
+        // the next strip into LDS, then this strip's stores: a wave's stores
+        // and loads share one completion counter, so stores issued before the
+        // wait for the staging loads would be waited for too
         if (more) store(cur ^ 1);
+        if (wlive) {
+            if (EPI != EPI_QKV || role == 0) ws_flush<EPI, NT, 0>(ro, t);
+            else if (role == 1) ws_flush<EPI, NT, 1>(ro, t);
+            else ws_flush<EPI, NT, 2>(ro, t);
+        }
         __syncthreads();
         cur ^= 1;
     }
@@ -332,23 +527,27 @@ static void launch_epi(const GemmArgs& a, dim3 grid, hipStream_t s) {
 
 template <int EPI, int KS>
 static void launch_ws(const GemmArgs& a, hipStream_t s) {
+    constexpr int SR = EPI == EPI_QKV ? 32 : 64;
     // two workgroups per CU (256 CUs), ncg column groups per row worker, the
     // workers a multiple of the 8 XCDs and no more than the strips
     const int ncg = (a.N + 255) / 256;
-    const int nstrips = (a.M + WS_SR - 1) / WS_SR;
+    const int nstrips = (a.M + SR - 1) / SR;
     int workers = std::max(NXCD, (512 / ncg) / NXCD * NXCD);
     workers = std::min(workers, (nstrips + NXCD - 1) / NXCD * NXCD);
     dim3 grid((unsigned)(workers * ncg));
     if (a.rq_fast)
-        hipLaunchKernelGGL((k_gemm_ws<EPI, true, KS>), grid, dim3(256), 0, s, a, ncg);
+        hipLaunchKernelGGL((k_gemm_ws<EPI, true, KS, SR>), grid, dim3(256), 0, s, a, ncg);
     else
-        hipLaunchKernelGGL((k_gemm_ws<EPI, false, KS>), grid, dim3(256), 0, s, a, ncg);
+        hipLaunchKernelGGL((k_gemm_ws<EPI, false, KS, SR>), grid, dim3(256), 0, s, a, ncg);
 }
 
 template <int EPI>
 static bool try_ws(const GemmArgs& a, hipStream_t s) {
     static const bool off = getenv("CZIP_GEMM_TILED") != nullptr;
     if (off || a.N % 64 != 0 || (long long)a.N * a.K >= (1ll << 31) || a.M <= 0) return false;
+    // 32-bit buffer offsets: the output rows, and the cache span of one strip
+    if (64ll * a.ldo * (EPI == EPI_RAW ? 4 : 1) >= (1ll << 31)) return false;
+    if (EPI == EPI_QKV && ((long long)a.KH * a.TP * 64 >= (1ll << 24) || a.T > a.TP)) return false;
     switch (a.K) {
         case 384: launch_ws<EPI, 6>(a, s); return true;
         case 512: launch_ws<EPI, 8>(a, s); return true;
