@@ -589,38 +589,27 @@ __device__ __forceinline__ void unpack4s(unsigned w, int* o) {
     o[3] = (int)(int8_t)(w >> 24);
 }
 
-// rmsnorm.rs:40-75 for one element: clamp(sra_rne((x * w) * inv, 15)), |x * w * inv| < 2^30
-__device__ __forceinline__ int rms_el(int x, int w, int inv) { return clamp127(rne_shr(x * w * inv, 15)); }
+// rmsnorm.rs:40-75 for one element: clamp(sra_rne((x * w) * inv, 15)).  |x|, |w| <= 127 and
+// 1 <= inv <= 2^15, so x * w is an exact 24-bit multiply and (x * w) * (inv * 2^-15)
+// is exact in f64 with |.| < 2^15: its rint (half to even) is one FMA.
+__device__ __forceinline__ int rms_el(int x, int w, double inv_s15) {
+    return clamp127(rint_fma_i32((double)__mul24(x, w), inv_s15));
+}
 
-template <int NW, int CT, bool FAST>
-__global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t As[2][RBM * 64];
-    __shared__ unsigned red[NW][RBM];
-    __shared__ int inv_s[RBM];
+// Epilogue of the row GEMM for rows m0 .. m0 + 63 (all d columns in the
+// workgroup): requantize, residual add, both RMSNorms (model.rs:424-468).
+// Lane holds columns nb + 16 t + c4 .. +3 of rows m0 + 16 i + lr; w1r / w2r
+// are its columns' norm weights.  Its residual inputs (int16 stream or the
+// token's embedding row) are requested first so that their latency hides
+// behind step 1 and the first reduction; mid() runs after that reduction,
+// before the first store.
+template <int NW, int CT, bool FAST, class Mid>
+__device__ __forceinline__ void rn_epilogue(const RowGemmArgs& a, v4i (&acc)[4][CT], int m0, const unsigned (&w1r)[CT],
+                                            const unsigned (&w2r)[CT], unsigned (*red)[RBM], int* inv_s, Mid mid) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int m0 = blockIdx.x * RBM;
-    const int nb = wave * CT * 16;  // first output column of this wave
+    const int nb = wave * CT * 16;
     const int lr = lane & 15, c4 = (lane >> 4) * 4;
-
-    v4i acc[4][CT];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int t = 0; t < CT; t++) acc[i][t] = (v4i){0, 0, 0, 0};
-
-    rowblock_mma<CT>(a.A, a.M, a.K, a.W, a.d, m0, nb, As, acc);
-
-    // epilogue.  Lane holds columns nb + 16 t + c4 .. +3 of rows m0 + 16 i + lr.
-    // Its global operands (norm weights of its columns, residual input of its
-    // rows: int16 stream or the token's embedding row) are all requested first
-    // so that their latency hides behind steps 1 and the first reduction.
-    unsigned w1r[CT], w2r[CT];
     uint2 xr[4][CT];
-#pragma unroll
-    for (int t = 0; t < CT; t++) {
-        w1r[t] = *(const unsigned*)(a.w1 + nb + t * 16 + c4);
-        w2r[t] = *(const unsigned*)(a.w2 + nb + t * 16 + c4);
-    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int row = min(m0 + i * 16 + lr, a.M - 1);
@@ -643,7 +632,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
             for (int r = 0; r < 4; r++) {
                 const int y = rq<FAST>(acc[i][t][r], a.rq_scale, a.mult, a.shift);
                 acc[i][t][r] = y;
-                ss += (unsigned)(y * y);
+                ss += (unsigned)__mul24(y, y);
             }
         ss += (unsigned)__shfl_xor((int)ss, 16, 64);
         ss += (unsigned)__shfl_xor((int)ss, 32, 64);
@@ -661,12 +650,13 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
         __syncthreads();
     };
     row_inv();
+    mid();
     // 2. x = x_in + rmsnorm(y, w1); keep clamp(x); row sums of clamp(x)^2
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int row = m0 + i * 16 + lr;
         const bool live = row < a.M;
-        const int inv = inv_s[i * 16 + lr];
+        const double inv = (double)inv_s[i * 16 + lr] * (1.0 / 32768.0);
         unsigned ss = 0;
 #pragma unroll
         for (int t = 0; t < CT; t++) {
@@ -685,7 +675,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
                 xnw[r] = xo[r] + rms_el(acc[i][t][r], w1v[r], inv);
                 const int xc = clamp127(xnw[r]);
                 acc[i][t][r] = xc;
-                ss += (unsigned)(xc * xc);
+                ss += (unsigned)__mul24(xc, xc);
             }
             if (a.x_out && live)
                 *(uint2*)(a.x_out + (size_t)row * a.d + n) = make_uint2(((unsigned)xnw[0] & 0xFFFFu) | ((unsigned)xnw[1] << 16),
@@ -702,7 +692,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
     for (int i = 0; i < 4; i++) {
         const int row = m0 + i * 16 + lr;
         if (row >= a.M) continue;
-        const int inv = inv_s[i * 16 + lr];
+        const double inv = (double)inv_s[i * 16 + lr] * (1.0 / 32768.0);
 #pragma unroll
         for (int t = 0; t < CT; t++) {
             const int n = nb + t * 16 + c4;
@@ -715,9 +705,127 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
     }
 }
 
+template <int NW, int CT, bool FAST>
+__global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) int8_t As[2][RBM * 64];
+    __shared__ unsigned red[NW][RBM];
+    __shared__ int inv_s[RBM];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int m0 = blockIdx.x * RBM;
+    const int nb = wave * CT * 16;  // first output column of this wave
+    const int c4 = (lane >> 4) * 4;
+
+    v4i acc[4][CT];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int t = 0; t < CT; t++) acc[i][t] = (v4i){0, 0, 0, 0};
+
+    rowblock_mma<CT>(a.A, a.M, a.K, a.W, a.d, m0, nb, As, acc);
+    unsigned w1r[CT], w2r[CT];
+#pragma unroll
+    for (int t = 0; t < CT; t++) {
+        w1r[t] = *(const unsigned*)(a.w1 + nb + t * 16 + c4);
+        w2r[t] = *(const unsigned*)(a.w2 + nb + t * 16 + c4);
+    }
+    rn_epilogue<NW, CT, FAST>(a, acc, m0, w1r, w2r, red, inv_s, [] {});
+}
+
+// ---------------------------------------------------------------------------
+// Persistent W-stationary row GEMM for K = 64 KS: each wave keeps its CT
+// column tiles of W for the whole K in registers (loaded once), one workgroup
+// per CU walks 64-row strips, the next strip's A fetched into registers while
+// the current one (double-buffered in LDS) is multiplied and written to LDS
+// between the epilogue's first reduction and its first store.
+// ---------------------------------------------------------------------------
+template <int NW, int CT, int KS, bool FAST>
+__global__ __launch_bounds__(64 * NW) void k_gemm_rn_ws(RowGemmArgs a) {
+    constexpr int K = KS * 64, KPT = 4 * KS / NW;  // staging loads per thread
+    static_assert(KPT * NW == 4 * KS, "a strip is 256 KS 16-byte chunks");
+    __shared__ __attribute__((aligned(16))) int8_t As[2][KS * RBM * 64];
+    __shared__ unsigned red[NW][RBM];
+    __shared__ int inv_s[RBM];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15;
+    const int nb = wave * CT * 16;
+    const int c4 = (lane >> 4) * 4;
+    const int nstrips = (a.M + RBM - 1) / RBM;
+    if ((int)blockIdx.x >= nstrips) return;  // the whole workgroup
+
+    v4i w[CT][KS];
+    {
+        const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)a.W, (short)0, a.d * K, BUF_DWORD3);
+        const int woff = (nb + lr) * K + (lane >> 4) * 16;
+#pragma unroll
+        for (int t = 0; t < CT; t++)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) w[t][ks] = __builtin_amdgcn_raw_buffer_load_b128(rW, woff + t * 16 * K, ks * 64, 0);
+    }
+    unsigned w1r[CT], w2r[CT];
+#pragma unroll
+    for (int t = 0; t < CT; t++) {
+        w1r[t] = *(const unsigned*)(a.w1 + nb + t * 16 + c4);
+        w2r[t] = *(const unsigned*)(a.w2 + nb + t * 16 + c4);
+    }
+    // staging: chunk c = tid + 64 NW n -> row (c / 4) % 64, 16-byte chunk c % 4 of K step c / 256
+    v4i st[KPT];
+    auto fetch = [&](int s) {
+        const int r0 = s * RBM;
+        const int rows = min(a.M - r0, RBM);
+        const __amdgpu_buffer_rsrc_t rA =
+            __builtin_amdgcn_make_buffer_rsrc((void*)(a.A + (size_t)r0 * K), (short)0, rows * K, BUF_DWORD3);
+#pragma unroll
+        for (int n = 0; n < KPT; n++) {
+            const int c = tid + 64 * NW * n;
+            st[n] = __builtin_amdgcn_raw_buffer_load_b128(rA, ((c >> 2) & 63) * K + (c & 3) * 16, (c >> 8) * 64, 0);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int n = 0; n < KPT; n++) {
+            const int c = tid + 64 * NW * n;
+            *(v4i*)(As[buf] + (c >> 8) * RBM * 64 + lds64((c >> 2) & 63, c & 3)) = st[n];
+        }
+    };
+    fetch(blockIdx.x);
+    store(0);
+    __syncthreads();
+    int cur = 0;
+    for (int s = blockIdx.x; s < nstrips; s += gridDim.x) {
+        const bool more = s + (int)gridDim.x < nstrips;
+        if (more) fetch(s + gridDim.x);
+        v4i acc[4][CT];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const v4i af = *(const v4i*)(As[cur] + ks * RBM * 64 + lds64(i * 16 + lr, lane >> 4));
+#pragma unroll
+                for (int t = 0; t < CT; t++)
+                    acc[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[t][ks], af, ks == 0 ? (v4i){0, 0, 0, 0} : acc[i][t],
+                                                                      0, 0, 0);
+            }
+        rn_epilogue<NW, CT, FAST>(a, acc, s * RBM, w1r, w2r, red, inv_s, [&] {
+            if (more) store(cur ^ 1);
+        });
+        __syncthreads();
+        cur ^= 1;
+    }
+}
+
 bool gemm_rn_supported(int d) {
     const int h = d / 64;
     return d % 64 == 0 && ((h >= 4 && h <= 8) || h == 10 || h == 12 || h == 14 || h == 16);
+}
+
+template <int NW, int CT, int KS>
+static void launch_rn_ws(const RowGemmArgs& a, hipStream_t s) {
+    // one workgroup per CU
+    const int nstrips = (a.M + RBM - 1) / RBM;
+    dim3 grid((unsigned)std::min(nstrips, 256));
+    if (a.rq_fast)
+        hipLaunchKernelGGL((k_gemm_rn_ws<NW, CT, KS, true>), grid, dim3(64 * NW), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_gemm_rn_ws<NW, CT, KS, false>), grid, dim3(64 * NW), 0, s, a);
 }
 
 template <int NW, int CT>
@@ -732,6 +840,11 @@ static void launch_rn(const RowGemmArgs& a, hipStream_t s) {
 // d = 64 h columns over NW waves of CT 16-wide tiles: 8 waves where h is even
 // (few accumulators per wave, many waves to hide the W stream's latency)
 void launch_gemm_rn(const RowGemmArgs& a, hipStream_t s) {
+    static const bool tiled = getenv("CZIP_GEMM_TILED") != nullptr;
+    if (!tiled && a.d == 384 && a.M > 0 && (long long)a.M * a.K < (1ll << 40)) {
+        if (a.K == 384) { launch_rn_ws<8, 3, 6>(a, s); return; }
+        if (a.K == 512) { launch_rn_ws<8, 3, 8>(a, s); return; }
+    }
     switch (a.d / 64) {
         case 4: launch_rn<8, 2>(a, s); break;
         case 5: launch_rn<4, 5>(a, s); break;
