@@ -196,6 +196,16 @@ __device__ __forceinline__ unsigned exp_q16_bf(int diff, const unsigned* lut32, 
     return diff >= 0 ? 65535u : x;
 }
 
+// The table step of exp_q16(-neg) for a coefficient below 2^24 (coef256 =
+// coef * 256): t = floor((neg * coef + 2^23) / 2^24) is the high word of
+// neg * coef256 + 2^31 (one 32 x 32 + 64 multiply-add), and every t >= 4352
+// (ip >= 17, result 1) gives the same result as t = 4352 (lut32[0] >> 17
+// rounds to 0), so clamping t replaces clamping ip.
+__device__ __forceinline__ unsigned exp_q16_t(unsigned neg, const unsigned* lut32, unsigned coef256) {
+    const unsigned t = min((unsigned)(((unsigned long long)neg * coef256 + 0x80000000ull) >> 32), 4352u);
+    return max(((lut32[t & 255u] >> (t >> 8)) + 0x8000u) >> 16, 1u);
+}
+
 // primitives.rs:163-185 (the result is formed with i32 wrap like `as i32 * sign`)
 __device__ __forceinline__ int div_rne_s32_u64(int num, unsigned long long den) {
     if (den == 0) return 0;

@@ -25,7 +25,8 @@ struct HeadLds {
 
 // Logits of the block (rowblock_mma), then per row, with two block reductions:
 //   1. max logit;
-//   2. first argmax (row_am) and S = sum E(l - max) (softmax_cdf.rs:96-110);
+//   2. first argmax (row_am) and S = sum E(l - max) (softmax_cdf.rs:96-110,
+//      coef < 2^24);
 // and every element's frequency f = 1 + e*Q + floor(e*Rm / S) (Q = R / S,
 // Rm = R % S, R = total - V) in place of its logit.  floor(e*Rm/S) is
 // floor(fma(e*Rm, 1/S, 2^-30)) in f64: e*Rm < 2^42 is exact, a nonzero
@@ -79,7 +80,8 @@ __device__ __forceinline__ void head_freqs(const int8_t* A, int M, int K, const 
                 const int col = nb + t * 16 + c4 + r;
                 const int l = acc[i][t][r];
                 am = (l == mx && col < am) ? col : am;
-                const unsigned e = exp_q16_bf((int)((unsigned)l - (unsigned)mx), L.lut32, coef);
+                const unsigned x = exp_q16_t((unsigned)mx - (unsigned)l, L.lut32, coef << 8);
+                const unsigned e = l == mx ? 65535u : x;  // E(0) is 65535 whatever lut[0]
                 acc[i][t][r] = (int)e;
                 s += e;
             }
