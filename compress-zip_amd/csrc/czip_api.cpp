@@ -24,6 +24,7 @@ constexpr uint32_t BOS = 1022u;  // main.rs:222, 387
 struct DevLayer {
     int8_t *attn_norm = nullptr, *post_attn_norm = nullptr, *ffn_norm = nullptr, *post_ffn_norm = nullptr;
     int8_t *qkv_w = nullptr, *out_w = nullptr, *up_w = nullptr, *down_w = nullptr, *sink = nullptr;
+    int8_t *out_wf = nullptr, *down_wf = nullptr;  // fragment-major copies (row GEMM)
     int32_t* score_mult = nullptr;
     int qkv_mult, out_mult, up_mult, down_mult, qkv_shift, out_shift, up_shift, down_shift;
     int qkv_n;  // QKV rows the attention reads
@@ -74,7 +75,7 @@ struct czip_ctx {
     bool rn_fused = false;  // residual + norms fused into the row GEMM (gemm_rn_supported(d_model))
     bool head_fused = false;  // LM head fused with the coder interval stage / decode step (head_cdf_supported(vocab))
     std::vector<void*> allocs;
-    int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr;
+    int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr, *head_wf = nullptr;
     uint16_t* lut = nullptr;
     int16_t *rcos = nullptr, *rsin = nullptr;
     std::vector<DevLayer> layers;
@@ -149,6 +150,20 @@ czip_status upload(czip_ctx* c, T** dst, const T* src, size_t count) {
     if (rc) return rc;
     HIPCHECK(c, hipMemcpy(*dst, src, count * sizeof(T), hipMemcpyHostToDevice));
     return CZIP_OK;
+}
+
+// W [N, K] in the fragment-major order of rowblock_mma (N % 16 == 0, K % 64
+// == 0): operand (tile t, K step s) at (t * K / 64 + s) * 1024, lane l's 16
+// bytes at +16 l = W[16 t + l % 16, 64 s + 16 (l / 16) .. +16].
+czip_status upload_frag_major(czip_ctx* c, int8_t** dst, const int8_t* W, size_t N, size_t K) {
+    if (N % 16 != 0 || K % 64 != 0) return fail(c, CZIP_E_CONFIG, "weight shape not a multiple of 16 x 64");
+    std::vector<int8_t> f(N * K);
+    const size_t ns = K / 64;
+    for (size_t t = 0; t < N / 16; t++)
+        for (size_t s = 0; s < ns; s++)
+            for (size_t l = 0; l < 64; l++)
+                memcpy(&f[(t * ns + s) * 1024 + l * 16], W + (16 * t + l % 16) * K + 64 * s + 16 * (l / 16), 16);
+    return upload(c, dst, f.data(), N * K);
 }
 
 // --- launch instrumentation ---
@@ -288,6 +303,7 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
     UP(c->embed, w->embed, V * d)
     UP(c->final_norm, w->final_norm, d)
     UP(c->head_w, w->head_w, V * d)
+    if ((rc = upload_frag_major(C, &c->head_wf, w->head_w, V, d))) return rc;
     UP(c->lut, w->exp2_lut, 256)
     UP(c->rcos, w->rope_cos, (size_t)w->rope_len)
     UP(c->rsin, w->rope_sin, (size_t)w->rope_len)
@@ -306,6 +322,7 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
         UP(D.post_ffn_norm, L.post_ffn_norm, d)
         UP(D.qkv_w, L.qkv_w, (size_t)D.qkv_n * d)
         UP(D.out_w, L.out_w, d * d)
+        if ((rc = upload_frag_major(C, &D.out_wf, L.out_w, d, d))) return rc;
         // gate/up interleave in groups of 32 rows so one 64-wide GEMM tile holds matching pairs
         for (size_t grp = 0; grp < F / 32; grp++) {
             memcpy(&perm[(grp * 64) * d], L.up_w + (grp * 32) * d, 32 * d);
@@ -313,6 +330,7 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
         }
         UP(D.up_w, perm.data(), 2 * F * d)
         UP(D.down_w, L.down_w, d * F)
+        if ((rc = upload_frag_major(C, &D.down_wf, L.down_w, d, F))) return rc;
         UP(D.score_mult, L.score_mult, (size_t)w->n_heads)
         if (L.sink_key) { UP(D.sink, L.sink_key, 64) }
         D.attn_general = attention_needs_general(w->exp2_lut, L.score_mult, w->n_heads);
@@ -406,7 +424,7 @@ void post_attention(czip_ctx* c, czip_job* j, int l, int M) {
     const int8_t* next = last ? c->final_norm : c->layers[(size_t)l + 1].attn_norm;
     if (c->rn_fused) {
         RowGemmArgs o{};
-        o.A = j->attn; o.W = L.out_w; o.M = M; o.K = d; o.d = d;
+        o.A = j->attn; o.W = L.out_w; o.Wf = L.out_wf; o.M = M; o.K = d; o.d = d;
         set_requant(o, L.out_mult, L.out_shift);
         o.w1 = L.ffn_norm; o.w2 = L.post_attn_norm;
         o.x_in = l == 0 ? nullptr : j->x; o.tok = j->inp; o.embed = c->embed;
@@ -425,7 +443,7 @@ void post_attention(czip_ctx* c, czip_job* j, int l, int M) {
     { Timed t(c, "gemm_up"); launch_gemm(u, EPI_REGLU, s); }
     if (c->rn_fused) {
         RowGemmArgs dn{};
-        dn.A = j->r8; dn.W = L.down_w; dn.M = M; dn.K = F; dn.d = d;
+        dn.A = j->r8; dn.W = L.down_w; dn.Wf = L.down_wf; dn.M = M; dn.K = F; dn.d = d;
         set_requant(dn, L.down_mult, L.down_shift);
         dn.w1 = L.post_ffn_norm; dn.w2 = next;
         dn.x_in = j->x; dn.x_out = last ? nullptr : j->x; dn.xn = j->xn;
@@ -646,7 +664,7 @@ static czip_status run_compress(czip_job* j) {
         if (rc) return rc;
         if (c->head_fused) {
             HeadCdfArgs h{};
-            h.A = j->xn; h.W = c->head_w; h.M = M; h.K = c->cfg.d_model; h.V = V; h.targets = j->tgt; h.lens = j->lens;
+            h.A = j->xn; h.W = c->head_wf; h.M = M; h.K = c->cfg.d_model; h.V = V; h.targets = j->tgt; h.lens = j->lens;
             h.T = T; h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total;
             h.out = j->lohi_all; h.out_row0 = c0 * T;
             Timed t(c, "head_cdf");
@@ -808,7 +826,7 @@ static czip_status run_decompress(czip_job* j) {
             }
             if (c->head_fused) {
                 HeadDecArgs h{};
-                h.A = j->xn; h.W = c->head_w; h.M = S; h.K = d; h.V = V;
+                h.A = j->xn; h.W = c->head_wf; h.M = S; h.K = d; h.V = V;
                 h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total; h.p = p;
                 Timed t(c, "head_dec");
                 launch_head_dec(h, st, ds, s);

@@ -29,25 +29,32 @@ __device__ __forceinline__ int lds64(int r, int c) { return r * 64 + ((c ^ ((r >
 
 constexpr int BUF_DWORD3 = 0x00020000;  // word 3 of a raw buffer resource: 32-bit data format, no swizzle
 
+// Fragment-major weights: for W [N, K] (N % 16 == 0, K % 64 == 0) the MFMA
+// operand of rows 16 t .. 16 t + 15 at K step s is the 1 KB at
+// (t * K / 64 + s) * 1024, lane l's 16 bytes at +16 l being W[16 t + l % 16,
+// 64 s + 16 (l / 16) .. +16]: one operand load reads eight whole 128-byte
+// lines (the row-major operand touches half of 16 lines, and the other half
+// is gone from L1 by the next step).
+//
 // acc[i][t] += A[m0 + 16 i + l%16, :] . W[nb + 16 t + l%16, :] over K (a
-// multiple of 64) for a workgroup that owns 64 rows of A: the 64 x 64 A tile
-// of each K step goes through double-buffered LDS (threads 0..255 stage 16
-// bytes each; rows past M read as 0 by the buffer range check), and each wave
-// streams its own CT W tiles straight into registers, in two register sets so
-// that the next step's loads are in flight while the current one multiplies.
-// W is the first MFMA operand: lane l ends with columns nb + 16 t + 4 (l / 16)
-// .. +3 of rows m0 + 16 i + l % 16.
+// multiple of 64) for a workgroup that owns 64 rows of A, Wf fragment-major:
+// the 64 x 64 A tile of each K step goes through double-buffered LDS (threads
+// 0..255 stage 16 bytes each; rows past M read as 0 by the buffer range
+// check), and each wave streams its own CT W operands straight into
+// registers, in two register sets so that the next step's loads are in
+// flight while the current one multiplies.  W is the first MFMA operand: lane
+// l ends with columns nb + 16 t + 4 (l / 16) .. +3 of rows m0 + 16 i + l % 16.
 template <int CT>
-__device__ __forceinline__ void rowblock_mma(const int8_t* A, int M, int K, const int8_t* W, int wrows, int m0,
+__device__ __forceinline__ void rowblock_mma(const int8_t* A, int M, int K, const int8_t* Wf, int wrows, int m0,
                                              int nb, int8_t (*As)[64 * 64], v4i (&acc)[4][CT]) {
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15;
     const int nk = K / 64;
     const int arows = M - m0 < 64 ? M - m0 : 64;
     const __amdgpu_buffer_rsrc_t rA =
         __builtin_amdgcn_make_buffer_rsrc((void*)(A + (size_t)m0 * K), (short)0, arows * K, BUF_DWORD3);
-    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, wrows * K, BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)Wf, (short)0, wrows * K, BUF_DWORD3);
     const int aoff = (tid >> 2) * K + (tid & 3) * 16;
-    const int woff = (nb + lr) * K + (lane >> 4) * 16;
+    const int woff = (nb >> 4) * nk * 1024 + lane * 16;
     v4i ra = (v4i){0, 0, 0, 0};
     auto fetch_a = [&](int k0) {
         if (tid < 256) ra = __builtin_amdgcn_raw_buffer_load_b128(rA, aoff, k0, 0);
@@ -57,7 +64,7 @@ __device__ __forceinline__ void rowblock_mma(const int8_t* A, int M, int K, cons
     };
     auto fetch_w = [&](v4i* w, int k0) {
 #pragma unroll
-        for (int t = 0; t < CT; t++) w[t] = __builtin_amdgcn_raw_buffer_load_b128(rW, woff + t * 16 * K, k0, 0);
+        for (int t = 0; t < CT; t++) w[t] = __builtin_amdgcn_raw_buffer_load_b128(rW, woff + t * nk * 1024, (k0 >> 6) * 1024, 0);
     };
     auto step = [&](int kt, const v4i* wc, v4i* wn) {
         const bool more = kt + 1 < nk;

@@ -57,6 +57,7 @@ struct AttnArgs {
 struct RowGemmArgs {
     const int8_t* A;      // [M, K]
     const int8_t* W;      // [d, K]
+    const int8_t* Wf;     // the same, fragment-major (rowblock_mma)
     int M, K, d;
     int mult, shift;
     double rq_scale;
@@ -76,7 +77,7 @@ void launch_gemm_rn(const RowGemmArgs& a, hipStream_t s);
 // without the int32 logits leaving the chip; V in {512, 1024}.
 struct HeadCdfArgs {
     const int8_t* A;           // [M, K] final-normalized rows
-    const int8_t* W;           // [V, K] head weights
+    const int8_t* W;           // [V, K] head weights, fragment-major (rowblock_mma)
     int M, K, V;
     const uint32_t* targets;   // [M]
     const int32_t* lens;       // [M / T]
@@ -134,7 +135,7 @@ void launch_cdf_decode(const int32_t* logits, int S, int V, const uint16_t* lut,
 // kernel (head_cdf_supported(V)); A = the final-normalized rows [S, K]
 struct HeadDecArgs {
     const int8_t* A;
-    const int8_t* W;           // [V, K]
+    const int8_t* W;           // [V, K], fragment-major (rowblock_mma)
     int M, K, V;
     const uint16_t* lut;       // [256]
     unsigned coef, total;

@@ -167,8 +167,9 @@ def test_attention_general_path(amd, orc, tmp_path):
 
 def test_unfused_norm_path(amd, orc, tmp_path, monkeypatch):
     """The residual + RMSNorm row kernels that back the row GEMM where it has no
-    instance (three heads) or is switched off, in both passes; and the separate
-    LM head + interval kernels behind the fused head of compression."""
+    instance (three heads) or is switched off, in both passes; the separate
+    LM head + interval kernels behind the fused heads; and the tiled GEMMs
+    behind the W-stationary ones."""
     from czip_amd import synth
     path = synth.write_random_model(str(tmp_path / "h3.czm"), d=192, n_layers=2, n_heads=3, n_kv=1, d_ff=256,
                                     vocab=1024, ctx=128, seed=90)
@@ -179,11 +180,15 @@ def test_unfused_norm_path(amd, orc, tmp_path, monkeypatch):
     gm2 = amd.Model(amd.ModelWeights(MODEL_PATH))
     lens = [64, 40]
     toks = synth.zipf_ids(sum(lens), 1024, seed=92)
-    _say("compress shipped, unfused norms")
     ref = orc.Model.from_file(MODEL_PATH).compress_many(toks, 64, threads=2)
-    assert gm2.compress_chunks(toks, 64) == ref
-    out = gm2.decompress_chunks(ref, lens)
-    assert np.array_equal(out, toks)
+    for tiled in (False, True):
+        # W-stationary requant / raw-logit GEMMs, then the tiled ones
+        if tiled:
+            monkeypatch.setenv("CZIP_GEMM_TILED", "1")
+        _say(f"compress shipped, unfused norms, tiled GEMMs {tiled}")
+        assert gm2.compress_chunks(toks, 64) == ref
+        out = gm2.decompress_chunks(ref, lens)
+        assert np.array_equal(out, toks)
 
 
 def test_requant_general_path(amd, orc, tmp_path):
