@@ -35,7 +35,8 @@ constexpr int RS = 68;                // row stride (words) of the per-wave buff
 
 struct AttnWaveLds {
     unsigned buf[16][RS];    // scores [row][key]; then per pass: column sums [column][dim]
-    uint16_t ex[16][64];     // [row][key]: at a record key, the rescale factor (0: nothing to rescale)
+    uint16_t ex[16][72];     // [row][key]: at a record key, the rescale factor (0: nothing to rescale);
+                             // 144-byte rows: 16-byte stores of 16 rows hit 64 banks
     int nrec[16];            // records of each row in the tile
 };
 
