@@ -76,6 +76,7 @@ struct czip_ctx {
     bool head_fused = false;  // LM head fused with the coder interval stage / decode step (head_cdf_supported(vocab))
     std::vector<void*> allocs;
     int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr, *head_wf = nullptr;
+    int8_t* embed_xn = nullptr;  // rmsnorm(embed[v], layer 0's attn_norm) for every token v (rn_fused)
     uint16_t* lut = nullptr;
     int16_t *rcos = nullptr, *rsin = nullptr;
     std::vector<DevLayer> layers;
@@ -338,6 +339,19 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
         D.qkv_shift = L.qkv_shift; D.out_shift = L.out_shift; D.up_shift = L.up_shift; D.down_shift = L.down_shift;
     }
 #undef UP
+    if (c->rn_fused) {
+        // layer 0's normalized input depends on the token alone: normalize every
+        // vocabulary row once with the prefill's own kernel, and let the QKV
+        // GEMM gather its A rows from this table by token id
+        std::vector<uint32_t> iota(V);
+        for (size_t v = 0; v < V; v++) iota[v] = (uint32_t)v;
+        uint32_t* d_iota = nullptr;
+        if ((rc = upload(C, &d_iota, iota.data(), V))) return rc;
+        if ((rc = dalloc(C, C->allocs, &c->embed_xn, V * d))) return rc;
+        launch_embed_norm(d_iota, c->embed, c->layers[0].attn_norm, (int)V, (int)d, nullptr, c->embed_xn, c->stream);
+        HIPCHECK(C, hipGetLastError());
+        HIPCHECK(C, hipStreamSynchronize(c->stream));
+    }
     *out = c.release();
     return CZIP_OK;
 }
@@ -464,14 +478,15 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T, bool head = t
     const int M = nb * T;
     const int d = c->cfg.d_model, F = c->cfg.d_ff, V = c->cfg.vocab, H = c->cfg.n_heads;
     hipStream_t s = c->stream;
-    {
+    if (!c->rn_fused) {
         Timed t(c, "embed_norm");
-        launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, M, d, c->rn_fused ? nullptr : j->x, j->xn, s);
+        launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, M, d, j->x, j->xn, s);
     }
     for (int l = 0; l < c->cfg.n_layers; l++) {
         const DevLayer& L = c->layers[(size_t)l];
         GemmArgs g{};
         g.A = j->xn; g.W = L.qkv_w; g.M = M; g.N = L.qkv_n; g.K = d;
+        if (l == 0 && c->rn_fused) { g.A = c->embed_xn; g.a_rows = j->inp; g.a_nrows = V; }
         g.out8 = j->q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
         g.d = d; g.T = T; g.TP = pad64(T); g.pos = -1; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads; g.KH = c->KH;
         g.kc = j->kc; g.vc = j->vc; g.rcos = c->rcos; g.rsin = c->rsin;
@@ -805,13 +820,14 @@ static czip_status run_decompress(czip_job* j) {
         { Timed t(c, "dec_init"); launch_dec_init(st, ds, S, s); }
         for (int p = 0; p < steps; p++) {
             { Timed t(c, "dec_prep"); launch_dec_prep(ds, S, p, j->inp, s); }
-            { Timed t(c, "embed_norm"); launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, S, d, c->rn_fused ? nullptr : j->x, j->xn, s); }
+            if (!c->rn_fused) { Timed t(c, "embed_norm"); launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, S, d, j->x, j->xn, s); }
             for (int l = 0; l < c->cfg.n_layers; l++) {
                 const DevLayer& L = c->layers[(size_t)l];
                 int8_t* kc = j->kc + (size_t)l * layer_kv;
                 int8_t* vc = j->vc + (size_t)l * layer_kv;
                 GemmArgs g{};
                 g.A = j->xn; g.W = L.qkv_w; g.M = S; g.N = L.qkv_n; g.K = d;
+                if (l == 0 && c->rn_fused) { g.A = c->embed_xn; g.a_rows = j->inp; g.a_nrows = V; }
                 g.out8 = j->q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
                 g.d = d; g.T = TP; g.TP = TP; g.pos = p; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
                 g.KH = c->KH; g.kc = kc; g.vc = vc; g.rcos = c->rcos; g.rsin = c->rsin;

@@ -189,9 +189,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
         for (int j = 0; j < 4; j++) acc[i][j] = (v4i){0, 0, 0, 0};
 
     TileRegs ta, tw;
-    const __amdgpu_buffer_rsrc_t ra = tile_rsrc(a.A, a.M, a.K, m0), rw = tile_rsrc(a.W, a.N, a.K, n0);
+    const __amdgpu_buffer_rsrc_t rw = tile_rsrc(a.W, a.N, a.K, n0);
     const int voff = (tid >> 2) * a.K + (tid & 3) * 16, voff2 = voff + 64 * a.K;
-    fetch_tile(ra, voff, voff2, 0, ta);
+    // A rows gathered from a table: offsets from the table's start, rows past M out of range
+    __amdgpu_buffer_rsrc_t ra;
+    int aoff = voff, aoff2 = voff2;
+    if (a.a_rows) {
+        ra = __builtin_amdgcn_make_buffer_rsrc((void*)a.A, (short)0, a.a_nrows * a.K, BUF_DWORD3);
+        const int r1 = m0 + (tid >> 2), r2 = r1 + 64;
+        aoff = r1 < a.M ? (int)a.a_rows[r1] * a.K + (tid & 3) * 16 : 0x7FFFFF00;
+        aoff2 = r2 < a.M ? (int)a.a_rows[r2] * a.K + (tid & 3) * 16 : 0x7FFFFF00;
+    } else {
+        ra = tile_rsrc(a.A, a.M, a.K, m0);
+    }
+    fetch_tile(ra, aoff, aoff2, 0, ta);
     fetch_tile(rw, voff, voff2, 0, tw);
     store_tile(ta, As[0], tid);
     store_tile(tw, Ws[0], tid);
@@ -200,7 +211,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     for (int kt = 0; kt < nk; kt++) {
         const int cur = kt & 1;
         if (kt + 1 < nk) {  // the next K step, fetched while this one is multiplied
-            fetch_tile(ra, voff, voff2, (kt + 1) * BK, ta);
+            fetch_tile(ra, aoff, aoff2, (kt + 1) * BK, ta);
             fetch_tile(rw, voff, voff2, (kt + 1) * BK, tw);
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of this step's MFMAs
@@ -459,12 +470,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ws(GemmArgs a, int ncg) {
     v4i st[KPT];
     auto fetch = [&](int s) {
         const int r0 = s * SR;
-        const int rows = min(a.M - r0, SR);
-        const __amdgpu_buffer_rsrc_t rA =
-            __builtin_amdgcn_make_buffer_rsrc((void*)(a.A + (size_t)r0 * K), (short)0, rows * K, BUF_DWORD3);
+        __amdgpu_buffer_rsrc_t rA;
+        int off;
+        if (a.a_rows) {  // A rows gathered from a table; rows past M out of range
+            rA = __builtin_amdgcn_make_buffer_rsrc((void*)a.A, (short)0, a.a_nrows * K, BUF_DWORD3);
+            off = r0 + srow < a.M ? (int)a.a_rows[r0 + srow] * K + sch * 16 : 0x7FFFFF00;
+        } else {
+            const int rows = min(a.M - r0, SR);
+            rA = __builtin_amdgcn_make_buffer_rsrc((void*)(a.A + (size_t)r0 * K), (short)0, rows * K, BUF_DWORD3);
+            off = srow * K + sch * 16;
+        }
 #pragma unroll
-        for (int n = 0; n < KPT; n++)
-            st[n] = __builtin_amdgcn_raw_buffer_load_b128(rA, srow * K + sch * 16, (kg + n * (64 / SR)) * 64, 0);
+        for (int n = 0; n < KPT; n++) st[n] = __builtin_amdgcn_raw_buffer_load_b128(rA, off, (kg + n * (64 / SR)) * 64, 0);
     };
     auto store = [&](int buf) {
 #pragma unroll

@@ -15,7 +15,9 @@ enum GemmEpi : int {
 };
 
 struct GemmArgs {
-    const int8_t* A;  // [M, K] row-major
+    const int8_t* A;  // [M, K] row-major, or with a_rows a table of a_nrows rows
+    const uint32_t* a_rows;  // nullptr, or row r of the product reads row a_rows[r] of A (< a_nrows)
+    int a_nrows;
     const int8_t* W;  // [N, K] row-major (PyTorch "TN")
     int M, N, K;
     int32_t* out32;   // EPI_RAW  [M, ldo]
