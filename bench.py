@@ -76,6 +76,8 @@ def gemm_ops_per_token(cfg, kv_mode):
     per_layer = {"gemm_qkv": qkv_n * d, "gemm_o": d * d, "gemm_o_norm": d * d, "gemm_up": 2 * F * d,
                  "gemm_down": d * F, "gemm_down_norm": d * F}
     out = {k: 2 * v * cfg["n_layers"] for k, v in per_layer.items()}
+    # layer 0's QKV projection is a per-token table (qkv_table: RoPE and scatter only)
+    out["gemm_qkv"] = 2 * qkv_n * d * (cfg["n_layers"] - 1)
     out["gemm_head"] = 2 * V * d
     out["head_cdf"] = 2 * V * d
     return out
@@ -173,7 +175,7 @@ def main():
     ops = gemm_ops_per_token(cfg, kv_mode)
     nrows = ((n + chunk - 1) // chunk) * chunk
     kernels = {}
-    for name in ["prep", "embed_norm", "gemm_qkv", "attention", "gemm_o", "gemm_o_norm", "row_norm", "gemm_up",
+    for name in ["prep", "embed_norm", "qkv_table", "gemm_qkv", "attention", "gemm_o", "gemm_o_norm", "row_norm", "gemm_up",
                  "gemm_down", "gemm_down_norm", "gemm_head", "cdf", "head_cdf", "encode"]:
         launches, tot = model.kernel_stats(name)
         if launches:
@@ -224,7 +226,7 @@ def main():
         if text is not None and tokenizer.decode_bytes(back) != text:
             raise SystemExit("detokenized output differs from the input text")
         dk = {}
-        for name in ["dec_init", "dec_prep", "embed_norm", "gemm_qkv", "attn_decode", "gemm_o", "gemm_o_norm",
+        for name in ["dec_init", "dec_prep", "embed_norm", "qkv_table", "gemm_qkv", "attn_decode", "gemm_o", "gemm_o_norm",
                      "row_norm", "gemm_up", "gemm_down", "gemm_down_norm", "head_dec", "gemm_head", "cdf_decode"]:
             launches, tot = model.kernel_stats(name)
             if launches:

@@ -76,7 +76,8 @@ struct czip_ctx {
     bool head_fused = false;  // LM head fused with the coder interval stage / decode step (head_cdf_supported(vocab))
     std::vector<void*> allocs;
     int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr, *head_wf = nullptr;
-    int8_t* embed_xn = nullptr;  // rmsnorm(embed[v], layer 0's attn_norm) for every token v (rn_fused)
+    int8_t* embed_xn = nullptr;  // rmsnorm(embed[v], layer 0's attn_norm) for every token v
+    int8_t* qkv_tab = nullptr;   // layer 0's requantized QKV projection of embed_xn[v] (before RoPE)
     uint16_t* lut = nullptr;
     int16_t *rcos = nullptr, *rsin = nullptr;
     std::vector<DevLayer> layers;
@@ -339,16 +340,23 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
         D.qkv_shift = L.qkv_shift; D.out_shift = L.out_shift; D.up_shift = L.up_shift; D.down_shift = L.down_shift;
     }
 #undef UP
-    if (c->rn_fused) {
-        // layer 0's normalized input depends on the token alone: normalize every
-        // vocabulary row once with the prefill's own kernel, and let the QKV
-        // GEMM gather its A rows from this table by token id
+    {
+        // layer 0's normalized input, and so its QKV projection before RoPE,
+        // depend on the token alone: normalize every vocabulary row once with
+        // the prefill's own kernel and project the table with the QKV GEMM's
+        // requantization; per row only RoPE and the cache scatter remain
         std::vector<uint32_t> iota(V);
         for (size_t v = 0; v < V; v++) iota[v] = (uint32_t)v;
         uint32_t* d_iota = nullptr;
         if ((rc = upload(C, &d_iota, iota.data(), V))) return rc;
         if ((rc = dalloc(C, C->allocs, &c->embed_xn, V * d))) return rc;
         launch_embed_norm(d_iota, c->embed, c->layers[0].attn_norm, (int)V, (int)d, nullptr, c->embed_xn, c->stream);
+        const DevLayer& L0 = c->layers[0];
+        if ((rc = dalloc(C, C->allocs, &c->qkv_tab, V * (size_t)L0.qkv_n))) return rc;
+        GemmArgs g{};
+        g.A = c->embed_xn; g.W = L0.qkv_w; g.M = (int)V; g.N = L0.qkv_n; g.K = (int)d;
+        g.out8 = c->qkv_tab; g.ldo = L0.qkv_n; set_requant(g, L0.qkv_mult, L0.qkv_shift);
+        launch_gemm(g, EPI_REQ, c->stream);
         HIPCHECK(C, hipGetLastError());
         HIPCHECK(C, hipStreamSynchronize(c->stream));
     }
@@ -471,6 +479,27 @@ void post_attention(czip_ctx* c, czip_job* j, int l, int M) {
     }
 }
 
+// Layer 0's QKV: from the per-token table (RoPE + scatter), or the GEMM over
+// the gathered normalized embedding rows (CZIP_QKV_GEMM=1, or a launch too
+// large for the table kernel's 32-bit item index).
+void layer0_qkv(czip_ctx* c, GemmArgs& g, const uint32_t* tok, hipStream_t s) {
+    const DevLayer& L = c->layers[0];
+    const int NG = c->cfg.kv_mode == CZIP_KV_GQA ? c->cfg.n_kv_heads : 1;
+    const long long items = (long long)g.M * (8 * c->cfg.n_heads + 24 * NG);
+    if (getenv("CZIP_QKV_GEMM") == nullptr && items < (1ll << 31)) {
+        QkvTabArgs q{};
+        q.tab = c->qkv_tab; q.tok = tok; q.M = g.M; q.T = g.T; q.TP = g.TP; q.pos = g.pos;
+        q.H = c->cfg.n_heads; q.NG = NG; q.KH = c->KH; q.d = c->cfg.d_model; q.qkv_n = L.qkv_n;
+        q.rcos = c->rcos; q.rsin = c->rsin; q.q8 = g.out8; q.kc = g.kc; q.vc = g.vc;
+        Timed t(c, "qkv_table");
+        launch_qkv_table(q, s);
+        return;
+    }
+    g.A = c->embed_xn; g.a_rows = tok; g.a_nrows = c->cfg.vocab;
+    Timed t(c, "gemm_qkv");
+    launch_gemm(g, EPI_QKV, s);
+}
+
 // Run every layer on rows [0, nb*T) whose inputs are j->inp / j->lens; leaves
 // logits in j->logits (head), else the final-normalized rows in j->xn.
 // (model.rs:362-480 as batched launches)
@@ -486,11 +515,15 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T, bool head = t
         const DevLayer& L = c->layers[(size_t)l];
         GemmArgs g{};
         g.A = j->xn; g.W = L.qkv_w; g.M = M; g.N = L.qkv_n; g.K = d;
-        if (l == 0 && c->rn_fused) { g.A = c->embed_xn; g.a_rows = j->inp; g.a_nrows = V; }
         g.out8 = j->q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
         g.d = d; g.T = T; g.TP = pad64(T); g.pos = -1; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads; g.KH = c->KH;
         g.kc = j->kc; g.vc = j->vc; g.rcos = c->rcos; g.rsin = c->rsin;
-        { Timed t(c, "gemm_qkv"); launch_gemm(g, EPI_QKV, s); }
+        if (l == 0) {
+            layer0_qkv(c, g, j->inp, s);
+        } else {
+            Timed t(c, "gemm_qkv");
+            launch_gemm(g, EPI_QKV, s);
+        }
         AttnArgs a{};
         a.q = j->q8; a.kc = j->kc; a.vc = j->vc; a.TP = pad64(T); a.lens = j->lens; a.score_mult = L.score_mult;
         a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = M; a.T = T; a.H = H; a.G = c->cfg.n_kv_heads;
@@ -827,11 +860,15 @@ static czip_status run_decompress(czip_job* j) {
                 int8_t* vc = j->vc + (size_t)l * layer_kv;
                 GemmArgs g{};
                 g.A = j->xn; g.W = L.qkv_w; g.M = S; g.N = L.qkv_n; g.K = d;
-                if (l == 0 && c->rn_fused) { g.A = c->embed_xn; g.a_rows = j->inp; g.a_nrows = V; }
                 g.out8 = j->q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
                 g.d = d; g.T = TP; g.TP = TP; g.pos = p; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
                 g.KH = c->KH; g.kc = kc; g.vc = vc; g.rcos = c->rcos; g.rsin = c->rsin;
-                { Timed t(c, "gemm_qkv"); launch_gemm(g, EPI_QKV, s); }
+                if (l == 0) {
+                    layer0_qkv(c, g, j->inp, s);
+                } else {
+                    Timed t(c, "gemm_qkv");
+                    launch_gemm(g, EPI_QKV, s);
+                }
                 AttnArgs a{};
                 a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = j->d_ntok + g0; a.score_mult = L.score_mult;
                 a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = S; a.T = TP; a.H = H; a.G = c->cfg.n_kv_heads;

@@ -92,6 +92,23 @@ struct HeadCdfArgs {
 bool head_cdf_supported(int V);
 void launch_head_cdf(const HeadCdfArgs& a, hipStream_t s);
 
+// Layer 0's Q/K/V from a per-token table: tab[v] = the requantized QKV
+// projection of token v's normalized embedding (before RoPE); per row: RoPE
+// on Q (two roundings) and K, scatter of K and V into the caches (the QKV
+// GEMM's epilogue, attention.rs:29-83).
+struct QkvTabArgs {
+    const int8_t* tab;       // [vocab, qkv_n]: Q heads | K heads | V heads
+    const uint32_t* tok;     // [M]
+    int M, T, TP, pos;       // pos >= 0: every row at pos, row = stream (decode)
+    int H, NG, KH, d, qkv_n; // NG = KV heads in the table
+    const int16_t* rcos;
+    const int16_t* rsin;
+    int8_t* q8;              // [M, d]
+    int8_t* kc;              // [B, KH, T, 64]
+    int8_t* vc;              // [B, KH, TP/16, 64, 16]
+};
+void launch_qkv_table(const QkvTabArgs& a, hipStream_t s);
+
 void launch_prep_chunks(const uint32_t* toks, int64_t n_tokens, int64_t chunk0, int nb, int T,
                         uint32_t* inp, uint32_t* tgt, int32_t* lens, hipStream_t s);
 // x may be nullptr (the residual stream is re-read from the embedding rows)

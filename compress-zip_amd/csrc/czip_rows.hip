@@ -142,6 +142,143 @@ void launch_embed_norm(const uint32_t* inp, const int8_t* embed, const int8_t* w
     hipLaunchKernelGGL(k_embed_norm, dim3((unsigned)((M + 15) / 16)), dim3(256), 0, s, inp, embed, w, M, d, x, xn);
 }
 
+// ---------------------------------------------------------------------------
+// Layer 0's QKV from the per-token table.  One thread per (row, item): items
+// 0 .. 8H-1 are query rotary groups (head i / 8, dims 4 (i % 8) .. +3 paired
+// with +32), the next 8 NG key rotary groups, the last 16 NG value quads.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_qkv_table(QkvTabArgs a) {
+    const int per_row = 8 * a.H + 24 * a.NG;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= a.M * per_row) return;
+    const int row = idx / per_row, it = idx - row * per_row;
+    const int b = a.pos >= 0 ? row : row / a.T, p = a.pos >= 0 ? a.pos : row - b * a.T;
+    const int8_t* t = a.tab + (size_t)a.tok[row] * a.qkv_n;
+    if (it >= 8 * a.H + 8 * a.NG) {  // V: dims 4 q .. 4 q + 3 of head g, [key/16][dim][16]
+        const int v = it - 8 * a.H - 8 * a.NG, g = v >> 4, q = v & 15;
+        const unsigned w = *(const unsigned*)(t + a.d + 64 * a.NG + 64 * g + 4 * q);
+        int8_t* dst = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP + (size_t)(p >> 4) * 1024 + (p & 15) + 4 * q * 16;
+#pragma unroll
+        for (int r = 0; r < 4; r++) dst[r * 16] = (int8_t)(w >> (8 * r));
+        return;
+    }
+    const bool isq = it < 8 * a.H;
+    const int hd = isq ? it >> 3 : (it - 8 * a.H) >> 3, i0 = 4 * (it & 7);
+    const int col = isq ? 64 * hd : a.d + 64 * hd;
+    const unsigned xw = *(const unsigned*)(t + col + i0), yw = *(const unsigned*)(t + col + i0 + 32);
+    const uint2 cw = *(const uint2*)(a.rcos + p * 32 + i0), sw = *(const uint2*)(a.rsin + p * 32 + i0);
+    int xq[4], yq[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int xv = (int8_t)(xw >> (8 * r)), yv = (int8_t)(yw >> (8 * r));
+        const unsigned cc = r < 2 ? cw.x : cw.y, ss = r < 2 ? sw.x : sw.y;
+        const int c = (int16_t)(r & 1 ? cc >> 16 : cc & 0xFFFFu), sn = (int16_t)(r & 1 ? ss >> 16 : ss & 0xFFFFu);
+        const int xr = (int)((unsigned)(xv * c) - (unsigned)(yv * sn));
+        const int yr = (int)((unsigned)(xv * sn) + (unsigned)(yv * c));
+        if (isq) {  // attention.rs:53-83 (>>15 then NET_SHIFT=1)
+            xq[r] = clamp127(rne_shr(rne_shr(xr, 15), 1));
+            yq[r] = clamp127(rne_shr(rne_shr(yr, 15), 1));
+        } else {    // attention.rs:29-50
+            xq[r] = clamp127(rne_shr(xr, 15));
+            yq[r] = clamp127(rne_shr(yr, 15));
+        }
+    }
+    int8_t* dst = isq ? a.q8 + (size_t)row * a.d + 64 * hd : a.kc + (((size_t)b * a.KH + hd) * a.T + p) * 64;
+    *(unsigned*)(dst + i0) = pack4(xq);
+    *(unsigned*)(dst + i0 + 32) = pack4(yq);
+}
+
+// Prefill: a workgroup takes 16 consecutive positions p0 .. p0 + 15 of one
+// chunk (p0 % 16 == 0), computes their Q and K rotary groups and gathers
+// their V rows into LDS, then writes every output as contiguous 16-byte
+// pieces: the 16 query rows (16 d bytes), each key head's 16 rows (1 KB) and
+// each value head's 64 x 16-key block of the transposed cache (1 KB).  Keys
+// past the chunk's T inside the last block get don't-care bytes (never
+// weighted by the attention).
+constexpr int QT_MAXD = 1024, QT_MAXG = 4;
+__global__ __launch_bounds__(256) void k_qkv_table_blk(QkvTabArgs a) {
+    __shared__ __attribute__((aligned(16))) int8_t qs[16 * QT_MAXD];
+    __shared__ __attribute__((aligned(16))) int8_t ks[QT_MAXG * 16 * 64];
+    __shared__ __attribute__((aligned(16))) int8_t vs[QT_MAXG * 16 * 64];
+    __shared__ uint32_t tk[16];
+    const int tid = threadIdx.x;
+    const int nkb = (a.T + 15) / 16;
+    const int b = blockIdx.x / nkb, p0 = (blockIdx.x - b * nkb) * 16;
+    const int nrows = min(16, a.T - p0);
+    const int row0 = b * a.T + p0;
+    if (tid < 16) tk[tid] = tid < nrows ? a.tok[row0 + tid] : 0u;
+    __syncthreads();
+    // Q and K rotary groups: item = (row k, group i): group < 8H query, else key
+    const int per_row = 8 * a.H + 8 * a.NG;
+    for (int idx = tid; idx < 16 * per_row; idx += 256) {
+        const int k = idx / per_row, it = idx - k * per_row;
+        const int8_t* t = a.tab + (size_t)tk[k] * a.qkv_n;
+        const bool isq = it < 8 * a.H;
+        const int hd = isq ? it >> 3 : (it - 8 * a.H) >> 3, i0 = 4 * (it & 7);
+        const int col = isq ? 64 * hd : a.d + 64 * hd;
+        const unsigned xw = *(const unsigned*)(t + col + i0), yw = *(const unsigned*)(t + col + i0 + 32);
+        const int p = min(p0 + k, a.T - 1);
+        const uint2 cw = *(const uint2*)(a.rcos + p * 32 + i0), sw = *(const uint2*)(a.rsin + p * 32 + i0);
+        int xq[4], yq[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int xv = (int8_t)(xw >> (8 * r)), yv = (int8_t)(yw >> (8 * r));
+            const unsigned cc = r < 2 ? cw.x : cw.y, ss = r < 2 ? sw.x : sw.y;
+            const int c = (int16_t)(r & 1 ? cc >> 16 : cc & 0xFFFFu), sn = (int16_t)(r & 1 ? ss >> 16 : ss & 0xFFFFu);
+            const int xr = (int)((unsigned)(xv * c) - (unsigned)(yv * sn));
+            const int yr = (int)((unsigned)(xv * sn) + (unsigned)(yv * c));
+            if (isq) {  // attention.rs:53-83 (>>15 then NET_SHIFT=1)
+                xq[r] = clamp127(rne_shr(rne_shr(xr, 15), 1));
+                yq[r] = clamp127(rne_shr(rne_shr(yr, 15), 1));
+            } else {    // attention.rs:29-50
+                xq[r] = clamp127(rne_shr(xr, 15));
+                yq[r] = clamp127(rne_shr(yr, 15));
+            }
+        }
+        int8_t* dst = isq ? qs + k * a.d + 64 * hd : ks + (hd * 16 + k) * 64;
+        *(unsigned*)(dst + i0) = pack4(xq);
+        *(unsigned*)(dst + i0 + 32) = pack4(yq);
+    }
+    // V rows (16 bytes per item)
+    for (int idx = tid; idx < 16 * a.NG * 4; idx += 256) {
+        const int k = idx / (4 * a.NG), r = idx - k * 4 * a.NG, g = r >> 2, c = r & 3;
+        *(uint4*)(vs + (g * 16 + k) * 64 + 16 * c) =
+            *(const uint4*)(a.tab + (size_t)tk[k] * a.qkv_n + a.d + 64 * a.NG + 64 * g + 16 * c);
+    }
+    __syncthreads();
+    // query rows: nrows * d contiguous bytes
+    const int qn = nrows * a.d / 16;
+    for (int i = tid; i < qn; i += 256) *(uint4*)(a.q8 + (size_t)row0 * a.d + 16 * i) = *(const uint4*)(qs + 16 * i);
+    // key rows of each head: nrows * 64 contiguous bytes
+    for (int i = tid; i < a.NG * nrows * 4; i += 256) {
+        const int g = i / (nrows * 4), c = i - g * nrows * 4;
+        *(uint4*)(a.kc + (((size_t)b * a.KH + g) * a.T + p0) * 64 + 16 * c) = *(const uint4*)(ks + g * 1024 + 16 * c);
+    }
+    // value blocks: dim j of head g -> the 16 keys' bytes
+    for (int i = tid; i < a.NG * 64; i += 256) {
+        const int g = i >> 6, j = i & 63;
+        unsigned w[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int8_t* v = vs + (g * 16 + 4 * q) * 64 + j;
+            w[q] = (unsigned)(uint8_t)v[0] | ((unsigned)(uint8_t)v[64] << 8) | ((unsigned)(uint8_t)v[128] << 16) |
+                   ((unsigned)(uint8_t)v[192] << 24);
+        }
+        *(uint4*)(a.vc + ((size_t)b * a.KH + g) * 64 * a.TP + (size_t)(p0 >> 4) * 1024 + 16 * j) =
+            make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+void launch_qkv_table(const QkvTabArgs& a, hipStream_t s) {
+    if (a.pos < 0 && a.d <= QT_MAXD && a.NG <= QT_MAXG) {
+        const int nb = a.M / a.T, nkb = (a.T + 15) / 16;
+        hipLaunchKernelGGL(k_qkv_table_blk, dim3((unsigned)(nb * nkb)), dim3(256), 0, s, a);
+        return;
+    }
+    const long long n = (long long)a.M * (8 * a.H + 24 * a.NG);
+    hipLaunchKernelGGL(k_qkv_table, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+}
+
 // x += rmsnorm(y8, w1) (model.rs:429-434 / 463-468);
 // xn = rmsnorm(clamp(x), w2) (model.rs:438-439, next layer 384-385, final 473-474)
 __global__ __launch_bounds__(256) void k_resid_norm(int16_t* __restrict__ x, const int8_t* __restrict__ y8,

@@ -168,8 +168,8 @@ def test_attention_general_path(amd, orc, tmp_path):
 def test_unfused_norm_path(amd, orc, tmp_path, monkeypatch):
     """The residual + RMSNorm row kernels that back the row GEMM where it has no
     instance (three heads) or is switched off, in both passes; the separate
-    LM head + interval kernels behind the fused heads; and the tiled GEMMs
-    behind the W-stationary ones."""
+    LM head + interval kernels behind the fused heads; the tiled GEMMs behind
+    the W-stationary ones; and layer 0's QKV GEMM behind its per-token table."""
     from czip_amd import synth
     path = synth.write_random_model(str(tmp_path / "h3.czm"), d=192, n_layers=2, n_heads=3, n_kv=1, d_ff=256,
                                     vocab=1024, ctx=128, seed=90)
@@ -177,6 +177,7 @@ def test_unfused_norm_path(amd, orc, tmp_path, monkeypatch):
     _check_logits(gm, om, 128, [128, 60], 91, 1024)
     monkeypatch.setenv("CZIP_UNFUSED_NORM", "1")
     monkeypatch.setenv("CZIP_UNFUSED_HEAD", "1")
+    monkeypatch.setenv("CZIP_QKV_GEMM", "1")  # layer 0's QKV by the GEMM over gathered rows, not the table
     gm2 = amd.Model(amd.ModelWeights(MODEL_PATH))
     lens = [64, 40]
     toks = synth.zipf_ids(sum(lens), 1024, seed=92)
