@@ -27,9 +27,8 @@ PEAK_HBM_GBS = 8000.0       # GB/s
 # HBM bytes per token (read + write) of each kernel on the text workload, from
 # two rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0: the factors a
 # plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text_1Mtok.md
-TRAFFIC_B_PER_TOKEN = {"attention": 514 + 384, "gemm_qkv": 389 + 513, "gemm_o_norm": 404 + 1152,
-                       "gemm_down_norm": 1816 + 384, "gemm_up": 390 + 1025, "head_cdf": 391 + 8,
-                       "embed_norm": 10 + 384}
+TRAFFIC_B_PER_TOKEN = {"attention": 514 + 384, "qkv_table": 12 + 512, "gemm_o_norm": 397 + 1152,
+                       "gemm_down_norm": 1816 + 384, "gemm_up": 570 + 1024, "head_cdf": 391 + 8}
 TRAFFIC_WORKLOADS = ("v001_L4_ctx512_text64MiB",)
 
 WORKLOADS = {
