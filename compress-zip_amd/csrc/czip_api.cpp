@@ -110,6 +110,8 @@ struct czip_job {
     int16_t* x = nullptr;  // residual stream (|x| <= 127 * (2 * n_layers + 1) < 2^15)
     int8_t *xn = nullptr, *q8 = nullptr, *kc = nullptr, *vc = nullptr, *attn = nullptr, *y8 = nullptr, *r8 = nullptr;
     int32_t* logits = nullptr;
+    int32_t* rn_ws = nullptr;  // split-K row GEMM workspace (decode with few streams)
+    size_t rn_ws_bytes = 0;
     // decompress
     int S = 0;  // streams decoded together
     int64_t total_tokens = 0;
@@ -450,7 +452,7 @@ void post_attention(czip_ctx* c, czip_job* j, int l, int M) {
         set_requant(o, L.out_mult, L.out_shift);
         o.w1 = L.ffn_norm; o.w2 = L.post_attn_norm;
         o.x_in = l == 0 ? nullptr : j->x; o.tok = j->inp; o.embed = c->embed;
-        o.x_out = j->x; o.xn = j->xn;
+        o.x_out = j->x; o.xn = j->xn; o.ws = j->rn_ws; o.ws_bytes = j->rn_ws_bytes;
         { Timed t(c, "gemm_o_norm"); launch_gemm_rn(o, s); }
     } else {
         GemmArgs o{};
@@ -468,7 +470,7 @@ void post_attention(czip_ctx* c, czip_job* j, int l, int M) {
         dn.A = j->r8; dn.W = L.down_w; dn.Wf = L.down_wf; dn.M = M; dn.K = F; dn.d = d;
         set_requant(dn, L.down_mult, L.down_shift);
         dn.w1 = L.post_ffn_norm; dn.w2 = next;
-        dn.x_in = j->x; dn.x_out = last ? nullptr : j->x; dn.xn = j->xn;
+        dn.x_in = j->x; dn.x_out = last ? nullptr : j->x; dn.xn = j->xn; dn.ws = j->rn_ws; dn.ws_bytes = j->rn_ws_bytes;
         { Timed t(c, "gemm_down_norm"); launch_gemm_rn(dn, s); }
     } else {
         GemmArgs dn{};
@@ -816,11 +818,13 @@ extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t* data, co
         (rc = dalloc(c, A, &j->q8, (size_t)S * d)) || (rc = dalloc(c, A, &j->attn, (size_t)S * d)) ||
         (rc = dalloc(c, A, &j->y8, (size_t)S * d)) || (rc = dalloc(c, A, &j->r8, (size_t)S * c->cfg.d_ff)) ||
         (rc = dalloc(c, A, &j->logits, c->head_fused ? 1 : (size_t)S * c->cfg.vocab)) ||
+        (rc = dalloc(c, A, &j->rn_ws, std::max<size_t>(gemm_rn_ws_bytes((int)S, (int)d) / 4, 1))) ||
         (rc = dalloc(c, A, &j->kc, L * (size_t)S * c->KH * pad64(Tcap) * 64)) ||
         (rc = dalloc(c, A, &j->vc, L * (size_t)S * c->KH * pad64(Tcap) * 64))) {
         free_job_mem(j.get());
         return rc;
     }
+    j->rn_ws_bytes = gemm_rn_ws_bytes((int)S, (int)d);
     hipError_t e = hipSuccess;
     if (total_bytes > 0) e = hipMemcpy(j->d_data, data, (size_t)total_bytes, hipMemcpyHostToDevice);
     if (e == hipSuccess && nchunks > 0) e = hipMemcpy(j->d_offs, offs, (size_t)nchunks * 8, hipMemcpyHostToDevice);

@@ -46,15 +46,18 @@ constexpr int BUF_DWORD3 = 0x00020000;  // word 3 of a raw buffer resource: 32-b
 // l ends with columns nb + 16 t + 4 (l / 16) .. +3 of rows m0 + 16 i + l % 16.
 template <int CT>
 __device__ __forceinline__ void rowblock_mma(const int8_t* A, int M, int K, const int8_t* Wf, int wrows, int m0,
-                                             int nb, int8_t (*As)[64 * 64], v4i (&acc)[4][CT]) {
+                                             int nb, int8_t (*As)[64 * 64], v4i (&acc)[4][CT], int ks0 = 0,
+                                             int nks = -1) {
+    // K steps ks0 .. ks0 + nks - 1 (all of them by default)
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15;
-    const int nk = K / 64;
+    const int nkt = K / 64;
+    const int nk = nks < 0 ? nkt : nks;
     const int arows = M - m0 < 64 ? M - m0 : 64;
     const __amdgpu_buffer_rsrc_t rA =
         __builtin_amdgcn_make_buffer_rsrc((void*)(A + (size_t)m0 * K), (short)0, arows * K, BUF_DWORD3);
     const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)Wf, (short)0, wrows * K, BUF_DWORD3);
-    const int aoff = (tid >> 2) * K + (tid & 3) * 16;
-    const int woff = (nb >> 4) * nk * 1024 + lane * 16;
+    const int aoff = (tid >> 2) * K + (tid & 3) * 16 + ks0 * 64;
+    const int woff = (nb >> 4) * nkt * 1024 + ks0 * 1024 + lane * 16;
     v4i ra = (v4i){0, 0, 0, 0};
     auto fetch_a = [&](int k0) {
         if (tid < 256) ra = __builtin_amdgcn_raw_buffer_load_b128(rA, aoff, k0, 0);
@@ -64,7 +67,7 @@ __device__ __forceinline__ void rowblock_mma(const int8_t* A, int M, int K, cons
     };
     auto fetch_w = [&](v4i* w, int k0) {
 #pragma unroll
-        for (int t = 0; t < CT; t++) w[t] = __builtin_amdgcn_raw_buffer_load_b128(rW, woff + t * nk * 1024, (k0 >> 6) * 1024, 0);
+        for (int t = 0; t < CT; t++) w[t] = __builtin_amdgcn_raw_buffer_load_b128(rW, woff + t * nkt * 1024, (k0 >> 6) * 1024, 0);
     };
     auto step = [&](int kt, const v4i* wc, v4i* wn) {
         const bool more = kt + 1 < nk;

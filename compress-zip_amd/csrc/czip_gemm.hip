@@ -829,6 +829,64 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn_ws(RowGemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Split-K row GEMM for few rows (decode with a few thousand streams): the
+// workgroup (row block, K slice) multiplies its K steps and stores the int32
+// partial sums; k_rn_splitk_epi then sums the slices and runs the row GEMM's
+// epilogue per row.  part: [splits][M][d].
+// ---------------------------------------------------------------------------
+template <int NW, int CT>
+__global__ __launch_bounds__(64 * NW) void k_gemm_rn_part(RowGemmArgs a, int ks_per, int32_t* __restrict__ part) {
+    __shared__ __attribute__((aligned(16))) int8_t As[2][RBM * 64];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int m0 = blockIdx.x * RBM, sp = blockIdx.y;
+    const int nb = wave * CT * 16;
+    const int lr = lane & 15, c4 = (lane >> 4) * 4;
+    const int ks0 = sp * ks_per, nks = min(ks_per, a.K / 64 - ks0);
+    v4i acc[4][CT];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int t = 0; t < CT; t++) acc[i][t] = (v4i){0, 0, 0, 0};
+    rowblock_mma<CT>(a.A, a.M, a.K, a.Wf, a.d, m0, nb, As, acc, ks0, nks);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = m0 + i * 16 + lr;
+        if (row < a.M) {
+#pragma unroll
+            for (int t = 0; t < CT; t++)
+                *(int4*)(part + ((size_t)sp * a.M + row) * a.d + nb + t * 16 + c4) =
+                    make_int4(acc[i][t][0], acc[i][t][1], acc[i][t][2], acc[i][t][3]);
+        }
+    }
+}
+
+constexpr int RN_MAX_SPLITS = 16;
+
+// K slices for M rows: enough (row block, slice) workgroups for the 256 CUs, at
+// least two K steps per slice; 1 = no split
+static int rn_splits(int M, int K) {
+    const int nblk = (M + RBM - 1) / RBM;
+    if (nblk >= 96) return 1;
+    return std::max(1, std::min(std::min(RN_MAX_SPLITS, K / 128), (384 + nblk - 1) / nblk));
+}
+
+size_t gemm_rn_ws_bytes(int M, int d) {
+    return (size_t)RN_MAX_SPLITS * (size_t)M * (size_t)d * 4u * ((M + RBM - 1) / RBM < 96 ? 1u : 0u);
+}
+
+template <int NW, int CT>
+static bool try_rn_splitk(const RowGemmArgs& a, hipStream_t s) {
+    const int splits = rn_splits(a.M, a.K);
+    if (splits < 2 || !a.ws || (size_t)splits * a.M * a.d * 4u > a.ws_bytes) return false;
+    const int ks_per = (a.K / 64 + splits - 1) / splits;
+    const int used = (a.K / 64 + ks_per - 1) / ks_per;  // slices that hold K steps
+    dim3 grid((unsigned)((a.M + RBM - 1) / RBM), (unsigned)used);
+    hipLaunchKernelGGL((k_gemm_rn_part<NW, CT>), grid, dim3(64 * NW), 0, s, a, ks_per, a.ws);
+    launch_rn_splitk_epi(a, a.ws, used, s);
+    return true;
+}
+
 bool gemm_rn_supported(int d) {
     const int h = d / 64;
     return d % 64 == 0 && ((h >= 4 && h <= 8) || h == 10 || h == 12 || h == 14 || h == 16);
@@ -847,6 +905,7 @@ static void launch_rn_ws(const RowGemmArgs& a, hipStream_t s) {
 
 template <int NW, int CT>
 static void launch_rn(const RowGemmArgs& a, hipStream_t s) {
+    if (try_rn_splitk<NW, CT>(a, s)) return;
     dim3 grid((unsigned)((a.M + RBM - 1) / RBM));
     if (a.rq_fast)
         hipLaunchKernelGGL((k_gemm_rn<NW, CT, true>), grid, dim3(64 * NW), 0, s, a);

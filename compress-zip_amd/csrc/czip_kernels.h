@@ -71,8 +71,13 @@ struct RowGemmArgs {
     const int8_t* embed;
     int16_t* x_out;        // [M, d] or nullptr (not needed after the last layer)
     int8_t* xn;            // [M, d]
+    int32_t* ws;           // optional workspace of ws_bytes for the split-K path (few rows)
+    size_t ws_bytes;
 };
 bool gemm_rn_supported(int d);
+// bytes of workspace the split-K row GEMM wants for M rows of width d (0: M is large enough without)
+size_t gemm_rn_ws_bytes(int M, int d);
+void launch_rn_splitk_epi(const RowGemmArgs& a, const int32_t* part, int splits, hipStream_t s);
 void launch_gemm_rn(const RowGemmArgs& a, hipStream_t s);
 
 // LM head + logits -> (cum_lo, cum_hi) of each row's target (k_cdf mode 0)

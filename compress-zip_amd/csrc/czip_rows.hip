@@ -143,6 +143,70 @@ void launch_embed_norm(const uint32_t* inp, const int8_t* embed, const int8_t* w
 }
 
 // ---------------------------------------------------------------------------
+// Epilogue of the split-K row GEMM, one wavefront per row: sum the K slices'
+// int32 partials (wrapping, like the accumulator), requantize, add the
+// residual (the int16 stream or the token's embedding row), both RMSNorms
+// (model.rs:424-468): the same arithmetic as the fused row GEMM's epilogue.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_rn_splitk_epi(RowGemmArgs a, const int32_t* __restrict__ part, int splits) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= a.M) return;
+    const int d = a.d, ng = d >> 2;
+    RowI8 yi, yn, xi;
+#pragma unroll
+    for (int j = 0; j < RG; j++) {
+        const int g = lane + 64 * j;
+        if (g < ng) {
+            unsigned acc[4] = {0u, 0u, 0u, 0u};
+            for (int sp = 0; sp < splits; sp++) {
+                const int4 v = *(const int4*)(part + ((size_t)sp * a.M + row) * d + 4 * g);
+                acc[0] += (unsigned)v.x; acc[1] += (unsigned)v.y; acc[2] += (unsigned)v.z; acc[3] += (unsigned)v.w;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                yi.v[j][k] = a.rq_fast ? clamp127(rint_fma_i32((double)(int)acc[k], a.rq_scale))
+                                       : requant((int)acc[k], a.mult, a.shift);
+        }
+    }
+    rms_row(yi, a.w1, d, lane, yn);
+    const int8_t* erow = a.x_in ? nullptr : a.embed + (size_t)a.tok[row] * d;
+#pragma unroll
+    for (int j = 0; j < RG; j++) {
+        const int g = lane + 64 * j;
+        if (g < ng) {
+            int xo[4];
+            if (a.x_in) {
+                const uint2 xv = *(const uint2*)(a.x_in + (size_t)row * d + 4 * g);
+                xo[0] = (int16_t)(xv.x & 0xFFFFu); xo[1] = (int16_t)(xv.x >> 16);
+                xo[2] = (int16_t)(xv.y & 0xFFFFu); xo[3] = (int16_t)(xv.y >> 16);
+            } else {
+                unpack4(*(const unsigned*)(erow + 4 * g), xo);
+            }
+            int nv[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                nv[k] = xo[k] + yn.v[j][k];
+                xi.v[j][k] = clamp127(nv[k]);
+            }
+            if (a.x_out)
+                *(uint2*)(a.x_out + (size_t)row * d + 4 * g) = make_uint2(((unsigned)nv[0] & 0xFFFFu) | ((unsigned)nv[1] << 16),
+                                                                          ((unsigned)nv[2] & 0xFFFFu) | ((unsigned)nv[3] << 16));
+        }
+    }
+    rms_row(xi, a.w2, d, lane, yn);
+#pragma unroll
+    for (int j = 0; j < RG; j++) {
+        const int g = lane + 64 * j;
+        if (g < ng) *(unsigned*)(a.xn + (size_t)row * d + 4 * g) = pack4(yn.v[j]);
+    }
+}
+
+void launch_rn_splitk_epi(const RowGemmArgs& a, const int32_t* part, int splits, hipStream_t s) {
+    hipLaunchKernelGGL(k_rn_splitk_epi, dim3((unsigned)((a.M + 3) / 4)), dim3(256), 0, s, a, part, splits);
+}
+
+// ---------------------------------------------------------------------------
 // Layer 0's QKV from the per-token table.  One thread per (row, item): items
 // 0 .. 8H-1 are query rotary groups (head i / 8, dims 4 (i % 8) .. +3 paired
 // with +32), the next 8 NG key rotary groups, the last 16 NG value quads.
