@@ -192,15 +192,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t rw = tile_rsrc(a.W, a.N, a.K, n0);
     const int voff = (tid >> 2) * a.K + (tid & 3) * 16, voff2 = voff + 64 * a.K;
     // A rows gathered from a table: offsets from the table's start, rows past M out of range
-    __amdgpu_buffer_rsrc_t ra;
+    const bool gather = a.a_rows != nullptr;
+    const __amdgpu_buffer_rsrc_t ra =
+        gather ? __builtin_amdgcn_make_buffer_rsrc((void*)a.A, (short)0, a.a_nrows * a.K, BUF_DWORD3)
+               : tile_rsrc(a.A, a.M, a.K, m0);
     int aoff = voff, aoff2 = voff2;
-    if (a.a_rows) {
-        ra = __builtin_amdgcn_make_buffer_rsrc((void*)a.A, (short)0, a.a_nrows * a.K, BUF_DWORD3);
+    if (gather) {
         const int r1 = m0 + (tid >> 2), r2 = r1 + 64;
         aoff = r1 < a.M ? (int)a.a_rows[r1] * a.K + (tid & 3) * 16 : 0x7FFFFF00;
         aoff2 = r2 < a.M ? (int)a.a_rows[r2] * a.K + (tid & 3) * 16 : 0x7FFFFF00;
-    } else {
-        ra = tile_rsrc(a.A, a.M, a.K, m0);
     }
     fetch_tile(ra, aoff, aoff2, 0, ta);
     fetch_tile(rw, voff, voff2, 0, tw);
@@ -470,18 +470,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ws(GemmArgs a, int ncg) {
     v4i st[KPT];
     auto fetch = [&](int s) {
         const int r0 = s * SR;
-        __amdgpu_buffer_rsrc_t rA;
-        int off;
-        if (a.a_rows) {  // A rows gathered from a table; rows past M out of range
-            rA = __builtin_amdgcn_make_buffer_rsrc((void*)a.A, (short)0, a.a_nrows * K, BUF_DWORD3);
-            off = r0 + srow < a.M ? (int)a.a_rows[r0 + srow] * K + sch * 16 : 0x7FFFFF00;
-        } else {
-            const int rows = min(a.M - r0, SR);
-            rA = __builtin_amdgcn_make_buffer_rsrc((void*)(a.A + (size_t)r0 * K), (short)0, rows * K, BUF_DWORD3);
-            off = srow * K + sch * 16;
-        }
+        // the resource from uniform values only (a per-lane choice of resource
+        // would make the compiler loop over distinct resources); with a_rows the
+        // A rows are gathered from a table, rows past M out of range
+        const bool gather = a.a_rows != nullptr;
+        const int8_t* base = gather ? a.A : a.A + (size_t)r0 * K;
+        const int nrec = gather ? a.a_nrows * K : min(a.M - r0, SR) * K;
+        const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, nrec, BUF_DWORD3);
+        int off = srow * K + sch * 16;
+        if (gather) off = r0 + srow < a.M ? (int)a.a_rows[r0 + srow] * K + sch * 16 : 0x7FFFFF00;
+        off += kg * 64;  // per lane in the vector offset; the scalar offset stays a constant
 #pragma unroll
-        for (int n = 0; n < KPT; n++) st[n] = __builtin_amdgcn_raw_buffer_load_b128(rA, off, (kg + n * (64 / SR)) * 64, 0);
+        for (int n = 0; n < KPT; n++) st[n] = __builtin_amdgcn_raw_buffer_load_b128(rA, off, n * (64 / SR) * 64, 0);
     };
     auto store = [&](int buf) {
 #pragma unroll
@@ -793,7 +793,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn_ws(RowGemmArgs a) {
 #pragma unroll
         for (int n = 0; n < KPT; n++) {
             const int c = tid + 64 * NW * n;
-            st[n] = __builtin_amdgcn_raw_buffer_load_b128(rA, ((c >> 2) & 63) * K + (c & 3) * 16, (c >> 8) * 64, 0);
+            st[n] = __builtin_amdgcn_raw_buffer_load_b128(rA, ((c >> 2) & 63) * K + (c & 3) * 16 + (c >> 8) * 64, 0, 0);
         }
     };
     auto store = [&](int buf) {
