@@ -11,6 +11,14 @@ namespace czip {
 // its 16 rows.
 // ---------------------------------------------------------------------------
 
+// K and V^T tiles in LDS: row r (64 bytes) of the tile at r * 64, its 16-byte
+// chunk c at slot c ^ swizzle.  The K tile is read in kperm order (lanes
+// 0..15 take rows 16 q + 4 blk + (0..3), q = lane / 4), the V^T tile in row
+// order; each swizzle spreads the 16 rows of a read, and the 4 rows x 4
+// chunks of a write, over distinct 16-byte bank groups.
+__device__ __forceinline__ int lds_k(int r, int c) { return r * 64 + ((c ^ ((r >> 4) & 3)) << 4); }
+__device__ __forceinline__ int lds_v(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
+
 template <bool GEN>
 __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     __shared__ unsigned lut32[256];
@@ -73,8 +81,8 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     for (int kt = 0; kt < ntiles; kt++) {
         const int t0 = kt * 64;
         __syncthreads();
-        *(v4i*)(Ks + lds64(ldr, tid & 3)) = kreg;
-        *(v4i*)(Vt + lds64(ldr, tid & 3)) = vreg;
+        *(v4i*)(Ks + lds_k(ldr, tid & 3)) = kreg;
+        *(v4i*)(Vt + lds_v(ldr, tid & 3)) = vreg;
         __syncthreads();
         if (kt + 1 < ntiles) {
             kreg = __builtin_amdgcn_raw_buffer_load_b128(rk, koff, (t0 + 64) * 64, 0);
@@ -83,9 +91,9 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
         if (!wave_live || t0 > wave_last) continue;
         int nvalid = p - (t0 + grp * 16) + 1;  // keys t <= p are visible (causal)
         nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
-        attn_tile<GEN, 1>([&](int, int blk) { return *(const v4i*)(Ks + lds64(blk * 16 + row, grp)); },
-                          [&](int, int db) { return *(const v4i*)(Vt + lds64(db * 16 + row, grp)); }, [] {}, &qop, 0,
-                          16, mscale, nvalid, t0 + 63 > wrow0, 16, lut32, W, st);
+        attn_tile<GEN, 1>([&](int, int blk) { return *(const v4i*)(Ks + lds_k(kperm(blk, row), grp)); },
+                          [&](int, int db) { return *(const v4i*)(Vt + lds_v(db * 16 + row, grp)); }, [] {}, &qop, 0,
+                          mscale, nvalid, t0 + 63 > wrow0, 16, lut32, W, st);
     }
     if (!wave_live) return;
     // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r

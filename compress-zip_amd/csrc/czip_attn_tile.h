@@ -34,10 +34,9 @@ constexpr unsigned WOFF = 32896;      // w - WOFF spans [-32896, 32639] = 256*[-
 constexpr int RS = 68;                // row stride (words) of the per-wave buffer: 16-byte accesses of 16 rows hit 64 banks
 
 struct AttnWaveLds {
-    unsigned buf[16][RS];    // scores [row][key]; then per pass: column sums [column][dim]
+    unsigned buf[16][RS];    // per pass: the segment sums [row][dim]
     uint16_t ex[16][72];     // [row][key]: at a record key, the rescale factor (0: nothing to rescale);
                              // 144-byte rows: 16-byte stores of 16 rows hit 64 banks
-    int nrec[16];            // records of each row in the tile
 };
 
 __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
@@ -68,6 +67,16 @@ __device__ __forceinline__ unsigned exp_neg(unsigned neg, const unsigned* lut32)
     return max(x, 1u);
 }
 
+// The same for the fast path, with the table index from a difference d of
+// two scores held in f64: t = floor(|d| * coef / 2^24 + 1/2) is one FMA
+// (|d| < 2^32 and coef < 2^19, so the sum is exact) truncated to u32, and
+// t >= 17 * 256 (ip >= 17) always gives 1, so t is capped there.
+__device__ __forceinline__ unsigned exp_neg_f(double d, const unsigned* lut32) {
+    const unsigned t = (unsigned)fmin(__builtin_fma(fabs(d), (double)ATTN_COEF_Q24 * 0x1p-24, 0.5), 4352.0);
+    const unsigned x = ((lut32[t & 255u] >> (t >> 8)) + 0x8000u) >> 16;
+    return max(x, 1u);
+}
+
 // vacc rescale at a record (attention.rs:246-261): the low 32 bits of
 // ((i64)v * e + (v >= 0 ? 2^15 : -2^15)) >> 16 (one 32x32+64 multiply-add)
 __device__ __forceinline__ unsigned rescale_v(unsigned v, unsigned e) {
@@ -82,14 +91,24 @@ __device__ __forceinline__ unsigned rescale_s(unsigned S, unsigned e) {
     return (unsigned)(((unsigned long long)S * e + 0x8000ull) >> 16);
 }
 
-// bytes of x equal to zero -> 0xFF, others -> 0x00 (exact per byte)
-__device__ __forceinline__ unsigned zero_bytes_mask(unsigned x) {
-    unsigned t = ((x & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | x;
-    t = ~t & 0x80808080u;
-    return (t >> 7) * 0xFFu;
-}
+// bit 7 of each byte of the result: that byte of x is zero (exact per byte;
+// the other bits are junk)
+__device__ __forceinline__ unsigned zero_bytes_b7(unsigned x) { return ~(((x & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | x); }
+
+// selector of v_perm_b32 that spreads bit 7 of each byte of z over the byte:
+// perm(z, z << 8, .) with selectors 8..11 = sign bits 15 and 31 of the low
+// operand and 15 and 31 of the high one, i.e. bits 7, 23, 15 and 31 of z;
+// selector 12 gives a zero byte
+constexpr unsigned SEL_B7 = 0x0B090A08u, SEL_ZERO = 0x0C0C0C0Cu;
+__device__ __forceinline__ unsigned spread_b7(unsigned z, unsigned sel) { return __builtin_amdgcn_perm(z, z << 8, sel); }
 
 __device__ __forceinline__ unsigned pick(unsigned msk, unsigned a, unsigned b) { return (a & msk) | (b & ~msk); }
+
+// The K operand's row m of MFMA block blk holds key kperm(blk, m) of the tile,
+// so that the score block's output lane (row, g) receives keys 16 g + 4 blk
+// + (0..3): after the 4 blocks each lane holds 16 consecutive keys of its
+// row, the order of the scan, with no transpose.
+__device__ __forceinline__ int kperm(int blk, int m) { return 16 * (m >> 2) + 4 * blk + (m & 3); }
 
 // Running state of a wave's 16 rows: max m and weight sum S with
 // lanes = rows (replicated over the 4 lane groups); vacc with lanes = head
@@ -100,7 +119,7 @@ struct AttnRows {
     unsigned vacc[16];
 };
 
-// One 64-key tile.  kop(s, blk): the K operand of keys 16*blk + lane%16,
+// One 64-key tile.  kop(s, blk): the K operand of key kperm(blk, lane%16),
 // head dims 16*(lane/16) .. +16; vop(s, db): the V^T operand of head dim
 // 16*db + lane%16, keys 16*(lane/16) .. +16 (each called once per index);
 // after_scan() runs once the scores have been scanned, before the V operands
@@ -110,36 +129,32 @@ struct AttnRows {
 // >= nrows are not combined into vacc (their m, S and vacc are unused).
 //
 // NS > 1 packs NS independent key streams (decode: streams sharing nothing
-// but the shape) into the wave's rows: rows [s*G, s*G + G) read stream s.
-// Every product is then summed over the streams with the other streams' rows
-// zeroed in the row-side operand (qs[s]: the lane's query when its row reads
-// stream s, else 0; rs: the lane's row's stream), so each row meets only its
-// own stream's keys and values: the streams are consecutive slices of the
-// contraction.  NS == 1: qs[0] is the query operand, rs and G are unused.
+// but the shape) into the wave's rows (rs: the lane's row's stream, NS for
+// none).  Every product is then summed over the streams, the streams being
+// consecutive slices of the contraction: the scores with the other streams'
+// rows zeroed in the query operand (qs[s]: the lane's query when its row
+// reads stream s, else 0), the PV products with weight 0 in the other
+// streams' columns (a constant, corrected like the keys outside a segment).
+// NS == 1: qs[0] is the query operand and rs is unused.
 template <bool GEN, int NS, class KOp, class VOp, class After>
-__device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan, const v4i* qs, int rs, int G,
-                                          double mscale, int nvalid, bool diag, int nrows, const unsigned* lut32,
-                                          AttnWaveLds& W, AttnRows& st) {
+__device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan, const v4i* qs, int rs, double mscale,
+                                          int nvalid, bool diag, int nrows, const unsigned* lut32, AttnWaveLds& W,
+                                          AttnRows& st) {
     const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
 
-    // 1. S^T = K Q^T, score epilogue, stored [row][key]
+    // 1. S^T = K Q^T and the score epilogue: lane (row, grp) gets the scores
+    // of keys 16*grp .. +16 of its row (kperm)
+    int sv[16];
 #pragma unroll
     for (int blk = 0; blk < 4; blk++) {
         v4i sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(0, blk), qs[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
         for (int t = 1; t < NS; t++) sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(t, blk), qs[t], sc, 0, 0, 0);
-        *(int4*)&W.buf[row][blk * 16 + grp * 4] = make_int4(score_b<GEN>(sc[0], mscale), score_b<GEN>(sc[1], mscale),
-                                                            score_b<GEN>(sc[2], mscale), score_b<GEN>(sc[3], mscale));
+#pragma unroll
+        for (int i = 0; i < 4; i++) sv[blk * 4 + i] = score_b<GEN>(sc[i], mscale);
     }
-    wave_lds_fence();
 
     // 2. in-order scan of keys [16*grp, 16*grp+16) of this row
-    int sv[16];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int4 v = *(const int4*)&W.buf[row][grp * 16 + i * 4];
-        sv[i * 4] = v.x; sv[i * 4 + 1] = v.y; sv[i * 4 + 2] = v.z; sv[i * 4 + 3] = v.w;
-    }
     if (diag) {
 #pragma unroll
         for (int k = 0; k < 16; k++)
@@ -156,33 +171,40 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
     if (grp >= 3) cur0 = max(cur0, e3);
     // weights and rescale factors: one exp per key, no branches, so the
     // 16 table reads can be in flight together
-    unsigned xs[16];
-    unsigned recm = 0u;   // bit k: key k is a record (weight 65535)
+    unsigned xs[16], ws[16];  // rescale factor (or weight) of each key, and its weight (65535 at a record)
+    unsigned recm = 0u;   // bit k: key k is a record
     unsigned fresh = 0u;  // bit k: key k is a record over "nothing seen": no rescale, no split
     int M = cur0;
+    double Mf = (double)cur0;  // fast path: the running max, in f64
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-        const int s = sv[k];
-        const bool rec = s > M;
+        const int s = sv[k], Mb = GEN ? M : cur0;  // fast path: Mb is only read at k == 0
+        bool rec;
         unsigned x;
         if (GEN) {
+            rec = s > M;
             const int d = (int)(rec ? (unsigned)M - (unsigned)s : (unsigned)s - (unsigned)M);  // i32 wrap, as the reference
             x = d >= 0 ? 65535u : exp_neg(0u - (unsigned)d, lut32);
+            M = max(M, s);
         } else {
-            x = exp_neg((unsigned)max(s, M) - (unsigned)min(s, M), lut32);
+            const double sf = (double)s;
+            rec = sf > Mf;
+            x = exp_neg_f(Mf - sf, lut32);
+            Mf = fmax(Mf, sf);
         }
+        ws[k] = rec ? 65535u : x;
         // a record over "nothing seen" has no rescale; in the fast path only
         // the lane's first key can meet M == INT32_MIN as a record (masked
         // keys are a suffix)
         if (GEN || k == 0) {
-            const bool f = rec && M == INT32_MIN;
+            const bool f = rec && Mb == INT32_MIN;
             x = f ? 0u : x;
             fresh |= (f ? 1u : 0u) << k;
         }
         xs[k] = x;
         recm |= (rec ? 1u : 0u) << k;
-        M = max(M, s);
     }
+    if (!GEN) M = max(cur0, bmax);
     // segments split at the records that rescale (a record over "nothing
     // seen" has nothing before it to rescale, so its segment runs on): the
     // row's splits in the tile (bit = key), their count and the splits before
@@ -209,9 +231,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
     unsigned hi_dw[4], lo_dw[4], sg_dw[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        unsigned w4[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) w4[k] = ((recm >> (i * 4 + k)) & 1u) ? 65535u : xs[i * 4 + k];
+        const unsigned* w4 = ws + i * 4;
         const unsigned p01 = __builtin_amdgcn_perm(w4[1], w4[0], 0x05010400u);
         const unsigned p23 = __builtin_amdgcn_perm(w4[3], w4[2], 0x05010400u);
         lo_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;
@@ -219,7 +239,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
         const unsigned nib = (splm >> (4 * i)) & 15u;
         const unsigned ones = (nib * 0x204081u) & 0x01010101u;  // bit k of nib -> byte k
         const unsigned base = seg + (unsigned)__builtin_popcount(splm & ((1u << (4 * i)) - 1u));
-        sg_dw[i] = ones * 0x01010101u + base * 0x01010101u;
+        sg_dw[i] = (ones + base) * 0x01010101u;  // byte k: base + bits 0..k of nib (all < 256)
     }
     if (diag) {  // invisible keys: weight 0 (bytes 0x80), no segment (0xFF)
 #pragma unroll
@@ -238,44 +258,56 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
 
     // 3. segment j of every row in pass j (MFMA column = row): O_j^T = V^T P_j^T
     after_scan();
-    if (grp == 0) W.nrec[row] = nrow;
     int nmax = nrow;
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
-    // A operand of the PV product, and the sum over the tile's 64 keys of v
-    // per stream (the product with a column of ones, moved to lanes = head dims)
+    // A operand of the PV product, and the sum over the tile's 64 keys (of
+    // every stream) of v at head dim = lane: rows of ones times V, whose
+    // output lane l holds column l % 16, i.e. dim 16 db + l % 16
+    constexpr v4i ONES = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
     v4i vop[NS][4];
+    int vsum = 0;
 #pragma unroll
-    for (int t = 0; t < NS; t++)
+    for (int db = 0; db < 4; db++) {
+        v4i cs = {0, 0, 0, 0};
 #pragma unroll
-        for (int db = 0; db < 4; db++) {
+        for (int t = 0; t < NS; t++) {
             vop[t][db] = vop_at(t, db);
-            const v4i cs = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                vop[t][db], (v4i){0x01010101, 0x01010101, 0x01010101, 0x01010101}, (v4i){0, 0, 0, 0}, 0, 0, 0);
-            if (row == 0) *(int4*)&W.buf[t][db * 16 + grp * 4] = make_int4(cs[0], cs[1], cs[2], cs[3]);
+            cs = __builtin_amdgcn_mfma_i32_16x16x64_i8(ONES, vop[t][db], cs, 0, 0, 0);
         }
-    wave_lds_fence();
-    unsigned corr[NS];
+        vsum = grp == db ? cs[0] : vsum;
+    }
+    // Every row's weight column for a stream other than its own reads w = 0
+    // (bytes -128, like the keys outside segment j), so each row's product
+    // carries -32896 * v of every key of every stream: one correction for
+    // all rows.  sel[t]: the byte-mask selector of stream t's column.
+    const unsigned corr = (unsigned)vsum * WOFF;
+    unsigned sel[NS];
 #pragma unroll
-    for (int t = 0; t < NS; t++) corr[t] = W.buf[t][lane] * WOFF;
-    int nr[16];
-#pragma unroll
-    for (int r = 0; r < 16; r++) nr[r] = __builtin_amdgcn_readfirstlane(W.nrec[r]);
+    for (int t = 0; t < NS; t++) sel[t] = NS == 1 || rs == t ? SEL_B7 : SEL_ZERO;
     for (int j = 0; j <= nmax; j++) {
         const unsigned jb = (unsigned)j * 0x01010101u;
-        v4i bh, bl;
-        int sh = 0, sl = 0;
+        v4i bhs[NS], bls[NS];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const unsigned msk = zero_bytes_mask(sg_dw[i] ^ jb);
-            bh[i] = (int)pick(msk, hi_dw[i], 0x80808080u);
-            bl[i] = (int)pick(msk, lo_dw[i], 0x80808080u);
-            sh = __builtin_amdgcn_sdot4(bh[i], 0x01010101, sh, false);
-            sl = __builtin_amdgcn_sdot4(bl[i], 0x01010101, sl, false);
+            const unsigned z = zero_bytes_b7(sg_dw[i] ^ jb);
+#pragma unroll
+            for (int t = 0; t < NS; t++) {
+                const unsigned msk = spread_b7(z, sel[t]);
+                bhs[t][i] = (int)pick(msk, hi_dw[i], 0x80808080u);
+                bls[t][i] = (int)pick(msk, lo_dw[i], 0x80808080u);
+            }
         }
-        int sw = sh * 256 + sl;  // sum over this lane's 16 keys of (w_j - 32896)
-        sw += __shfl_xor(sw, 16, 64);
-        sw += __shfl_xor(sw, 32, 64);
+        // sum over the row's 64 keys of (w_j - 32896) (rows of ones times the
+        // weight columns: output lane l holds column l % 16 = the lane's
+        // row), less the other streams' columns (64 keys of -32896 each)
+        v4i sh = {0, 0, 0, 0}, sl = {0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < NS; t++) {
+            sh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ONES, bhs[t], sh, 0, 0, 0);
+            sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(ONES, bls[t], sl, 0, 0, 0);
+        }
+        const int sw = sh[0] * 256 + sl[0] + (NS - 1) * 64 * (int)WOFF;
         // rescale factor of this lane's row at record j (0: none), the lowest
         // record not yet passed; row r's is read by the combine from lane r
         unsigned erow = 0u;
@@ -288,20 +320,6 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
         // 4a. S of this lane's row (lanes = rows): rescale at record j, then add segment j
         if (erow) st.S = rescale_s(st.S, erow);
         st.S += (unsigned)sw + 64u * WOFF;
-        // the weight columns per stream: the other streams' rows read 0
-        v4i bhs[NS], bls[NS];
-        if (NS == 1) {
-            bhs[0] = bh;
-            bls[0] = bl;
-        } else {
-#pragma unroll
-            for (int t = 0; t < NS; t++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    bhs[t][i] = rs == t ? bh[i] : 0;
-                    bls[t][i] = rs == t ? bl[i] : 0;
-                }
-        }
 #pragma unroll
         for (int db = 0; db < 4; db++) {
             v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[0][db], bhs[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
@@ -312,6 +330,10 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
             for (int t = 0; t < NS; t++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[t][db], bls[t], acc, 0, 0, 0);
             *(int4*)&W.buf[row][db * 16 + grp * 4] = make_int4(acc[0], acc[1], acc[2], acc[3]);
         }
+        // rows (bit r, from lane r) that have a segment j, and those that
+        // rescale first
+        const unsigned long long live = __builtin_amdgcn_ballot_w64(j <= nrow);
+        const unsigned long long resc = __builtin_amdgcn_ballot_w64(erow != 0u);
         wave_lds_fence();
         // 4b. vacc (lanes = head dims): every row that has a segment j
         unsigned bv[16];
@@ -320,13 +342,10 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
             if (r < nrows) bv[r] = W.buf[r][lane];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            if (r < nrows && j <= nr[r]) {
-                const unsigned e = (unsigned)__builtin_amdgcn_readlane((int)erow, r);
-                if (e) st.vacc[r] = rescale_v(st.vacc[r], e);
-                unsigned c = corr[0];
-#pragma unroll
-                for (int t = 1; t < NS; t++) c = r >= t * G ? corr[t] : c;
-                st.vacc[r] += bv[r] + c;
+            if (r < nrows && ((live >> r) & 1ull)) {
+                if ((resc >> r) & 1ull)
+                    st.vacc[r] = rescale_v(st.vacc[r], (unsigned)__builtin_amdgcn_readlane((int)erow, r));
+                st.vacc[r] += bv[r] + corr;
             }
         }
         wave_lds_fence();

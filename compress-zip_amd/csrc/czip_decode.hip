@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
         rv[t] = __builtin_amdgcn_make_buffer_rsrc((void*)(a.vc + base), (short)0, a.TP * 64, BUF_DWORD3);
     }
     auto load_k = [&](int t, int blk, int t0) {
-        return __builtin_amdgcn_raw_buffer_load_b128(rk[t], (t0 + blk * 16 + row) * 64 + grp * 16, 0, 0);
+        return __builtin_amdgcn_raw_buffer_load_b128(rk[t], (t0 + kperm(blk, row)) * 64 + grp * 16, 0, 0);
     };
     auto load_v = [&](int t, int db, int t0) {
         return __builtin_amdgcn_raw_buffer_load_b128(rv[t], ((t0 / 16 + grp) * 64 + db * 16 + row) * 16, 0, 0);
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
                     kn[blk] = load_k(0, blk, tn);
                     return kc[blk];
                 },
-                [&](int, int db) { return vc[db]; }, [] {}, qs, 0, G, mscale, nvalid_at(t0), t0 + 63 > p, G, lut32,
+                [&](int, int db) { return vc[db]; }, [] {}, qs, 0, mscale, nvalid_at(t0), t0 + 63 > p, G, lut32,
                 wl[wave], st);
 #pragma unroll
             for (int db = 0; db < 4; db++) vn[db] = load_v(0, db, tn);
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
 #pragma unroll
                         for (int blk = 0; blk < 4; blk++) kr[t][blk] = load_k(t, blk, tn);
                 },
-                qs, rs, G, mscale, nvalid_at(t0), t0 + 63 > p, NS * G, lut32, wl[wave], st);
+                qs, rs, mscale, nvalid_at(t0), t0 + 63 > p, NS * G, lut32, wl[wave], st);
 #pragma unroll
             for (int t = 0; t < NS; t++)
 #pragma unroll
