@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
         for (int i = 0; i < 4; i++) dot = __builtin_amdgcn_sdot4(qop[i], sk[i], dot, false);
         dot += __shfl_xor(dot, 16, 64);
         dot += __shfl_xor(dot, 32, 64);
-        st.m = score_b<GEN>(dot, mscale);
+        st.m = score_b<GEN>(dot, mscale, score_bias(mscale));
         st.S = 65535u;
     }
 

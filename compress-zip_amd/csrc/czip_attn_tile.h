@@ -41,15 +41,24 @@ struct AttnWaveLds {
 
 __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
-// sra_rne64(sra_rne32(dot, 2) * mult, 15) (attention.rs:233-239).
-// RNE of a quotient by 2^k is symmetric, so the floor form
-// (x + 2^(k-1) - 1 + bit_k(x)) >> k equals the reference's sign-magnitude one;
-// the product is exact in f64 and rint rounds half to even.
-// The fast path (|score| < 2^30) takes the rint from one FMA.
+// sra_rne64(sra_rne32(dot, 2) * mult, 15) (attention.rs:233-239), mscale =
+// mult * 2^-15.  RNE of a quotient by 2^k is symmetric, so it is IEEE
+// round-half-even.  Fast path (|score| < 2^30, |mult| < 2^27), two FMAs
+// around B = 1.5 * 2^52 (ulp 1): r1 = fma(dot, 1/4, B) = B + du exactly
+// (du = sra_rne32(dot, 2)), and fma(r1, mscale, cb) with cb = B * (1 -
+// mscale) (exact: 1.5 * 2^37 * (2^15 - mult)) is B + du * mscale rounded
+// once, whose low word is the score.  The general path rounds du * mscale
+// in f64 (exact, |du * mult| < 2^49) and clamps to the i32 range.
+__device__ __forceinline__ double score_bias(double mscale) {
+    return __builtin_fma(-6755399441055744.0, mscale, 6755399441055744.0);
+}
 template <bool GEN>
-__device__ __forceinline__ int score_b(int dot, double mscale) {
+__device__ __forceinline__ int score_b(int dot, double mscale, double cb) {
+    if (!GEN) {
+        const double r1 = __builtin_fma((double)dot, 0.25, 6755399441055744.0);
+        return (int)(unsigned)__builtin_bit_cast(unsigned long long, __builtin_fma(r1, mscale, cb));
+    }
     const int du = (dot + 1 + ((dot >> 2) & 1)) >> 2;
-    if (!GEN) return rint_fma_i32((double)du, mscale);
     double r = __builtin_rint((double)du * mscale);
     r = fmin(fmax(r, -2147483648.0), 2147483647.0);
     return (int)r;
@@ -71,10 +80,12 @@ __device__ __forceinline__ unsigned exp_neg(unsigned neg, const unsigned* lut32)
 // two scores held in f64: t = floor(|d| * coef / 2^24 + 1/2) is one FMA
 // (|d| < 2^32 and coef < 2^19, so the sum is exact) truncated to u32, and
 // t >= 17 * 256 (ip >= 17) always gives 1, so t is capped there.
-__device__ __forceinline__ unsigned exp_neg_f(double d, const unsigned* lut32) {
-    const unsigned t = (unsigned)fmin(__builtin_fma(fabs(d), (double)ATTN_COEF_Q24 * 0x1p-24, 0.5), 4352.0);
-    const unsigned x = ((lut32[t & 255u] >> (t >> 8)) + 0x8000u) >> 16;
-    return max(x, 1u);
+__device__ __forceinline__ unsigned exp_idx_f(double d) {
+    return (unsigned)fmin(__builtin_fma(fabs(d), (double)ATTN_COEF_Q24 * 0x1p-24, 0.5), 4352.0);
+}
+// the value from the table word at t & 255
+__device__ __forceinline__ unsigned exp_from(unsigned t, unsigned word) {
+    return max(((word >> (t >> 8)) + 0x8000u) >> 16, 1u);
 }
 
 // vacc rescale at a record (attention.rs:246-261): the low 32 bits of
@@ -145,13 +156,14 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
     // 1. S^T = K Q^T and the score epilogue: lane (row, grp) gets the scores
     // of keys 16*grp .. +16 of its row (kperm)
     int sv[16];
+    const double cb = score_bias(mscale);
 #pragma unroll
     for (int blk = 0; blk < 4; blk++) {
         v4i sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(0, blk), qs[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
         for (int t = 1; t < NS; t++) sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(t, blk), qs[t], sc, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; i++) sv[blk * 4 + i] = score_b<GEN>(sc[i], mscale);
+        for (int i = 0; i < 4; i++) sv[blk * 4 + i] = score_b<GEN>(sc[i], mscale, cb);
     }
 
     // 2. in-order scan of keys [16*grp, 16*grp+16) of this row
@@ -175,36 +187,51 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
     unsigned recm = 0u;   // bit k: key k is a record
     unsigned fresh = 0u;  // bit k: key k is a record over "nothing seen": no rescale, no split
     int M = cur0;
-    double Mf = (double)cur0;  // fast path: the running max, in f64
+    if (GEN) {
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        const int s = sv[k], Mb = GEN ? M : cur0;  // fast path: Mb is only read at k == 0
-        bool rec;
-        unsigned x;
-        if (GEN) {
-            rec = s > M;
+        for (int k = 0; k < 16; k++) {
+            const int s = sv[k];
+            const bool rec = s > M;
             const int d = (int)(rec ? (unsigned)M - (unsigned)s : (unsigned)s - (unsigned)M);  // i32 wrap, as the reference
-            x = d >= 0 ? 65535u : exp_neg(0u - (unsigned)d, lut32);
-            M = max(M, s);
-        } else {
-            const double sf = (double)s;
-            rec = sf > Mf;
-            x = exp_neg_f(Mf - sf, lut32);
-            Mf = fmax(Mf, sf);
-        }
-        ws[k] = rec ? 65535u : x;
-        // a record over "nothing seen" has no rescale; in the fast path only
-        // the lane's first key can meet M == INT32_MIN as a record (masked
-        // keys are a suffix)
-        if (GEN || k == 0) {
-            const bool f = rec && Mb == INT32_MIN;
+            unsigned x = d >= 0 ? 65535u : exp_neg(0u - (unsigned)d, lut32);
+            ws[k] = rec ? 65535u : x;
+            const bool f = rec && M == INT32_MIN;  // a record over "nothing seen" has no rescale
             x = f ? 0u : x;
             fresh |= (f ? 1u : 0u) << k;
+            xs[k] = x;
+            recm |= (rec ? 1u : 0u) << k;
+            M = max(M, s);
         }
-        xs[k] = x;
-        recm |= (rec ? 1u : 0u) << k;
+    } else {
+        // three phases, so that the 16 table reads are in flight together:
+        // the running max (f64) and every key's table index, the reads, the
+        // values.  Only the lane's first key can meet M == INT32_MIN as a
+        // record (masked keys are a suffix).
+        unsigned tk[16];
+        bool recb[16];
+        double Mf = (double)cur0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const double sf = (double)sv[k];
+            recb[k] = sf > Mf;
+            tk[k] = exp_idx_f(Mf - sf);
+            Mf = fmax(Mf, sf);
+            recm |= (recb[k] ? 1u : 0u) << k;
+        }
+        fresh = recb[0] && cur0 == INT32_MIN ? 1u : 0u;
+        __builtin_amdgcn_sched_barrier(0);
+        unsigned word[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) word[k] = lut32[tk[k] & 255u];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const unsigned x = exp_from(tk[k], word[k]);
+            ws[k] = recb[k] ? 65535u : x;
+            xs[k] = k == 0 && fresh ? 0u : x;
+        }
+        M = max(cur0, bmax);
     }
-    if (!GEN) M = max(cur0, bmax);
     // segments split at the records that rescale (a record over "nothing
     // seen" has nothing before it to rescale, so its segment runs on): the
     // row's splits in the tile (bit = key), their count and the splits before

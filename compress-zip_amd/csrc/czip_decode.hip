@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
         dot += __shfl_xor(dot, 16, 64);
         dot += __shfl_xor(dot, 32, 64);
         if (live) {
-            st.m = score_b<GEN>(dot, mscale);
+            st.m = score_b<GEN>(dot, mscale, score_bias(mscale));
             st.S = 65535u;
         }
     }
