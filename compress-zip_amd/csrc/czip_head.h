@@ -20,7 +20,7 @@ struct HeadLds {
     unsigned red_b[HNW][HBM_ROWS], red_c[HNW][HBM_ROWS];
     int row_i[HBM_ROWS], row_am[HBM_ROWS];
     unsigned row_Q[HBM_ROWS];
-    double row_Rm[HBM_ROWS], row_inv[HBM_ROWS];
+    double row_y[HBM_ROWS];
 };
 
 // Logits of the block (rowblock_mma), then per row, with two block reductions:
@@ -28,11 +28,12 @@ struct HeadLds {
 //   2. first argmax (row_am) and S = sum E(l - max) (softmax_cdf.rs:96-110,
 //      coef < 2^24);
 // and every element's frequency f = 1 + e*Q + floor(e*Rm / S) (Q = R / S,
-// Rm = R % S, R = total - V) in place of its logit.  floor(e*Rm/S) is
-// floor(fma(e*Rm, 1/S, 2^-30)) in f64: e*Rm < 2^42 is exact, a nonzero
-// fraction of e*Rm/S is >= 1/S >= 2^-26, and the f64 error of the product
-// with the rounded 1/S is < 2^-35 for quotients below 2^16.  The argmax's
-// remainder (total - sum f) is left to the caller.
+// Rm = R % S, R = total - V) in place of its logit.  1 + floor(e*Rm/S) is
+// the truncation of fma(e, y, 1 + 2^-30) in f64 with y = Rm / S correctly
+// rounded (|y - Rm/S| <= 2^-54, y < 1): the result is below 2^16 + 2, so
+// its error is < 2^16 * 2^-54 + 2^-37 < 2^-36, while a nonzero fraction of
+// e*Rm/S is >= 1/S >= 2^-26 (S < 2^26).  The argmax's remainder
+// (total - sum f) is left to the caller.
 template <int CT>
 __device__ __forceinline__ void head_freqs(const int8_t* A, int M, int K, const int8_t* W, int V, int m0,
                                            const uint16_t* lut, unsigned coef, unsigned total, HeadLds& L,
@@ -107,8 +108,7 @@ __device__ __forceinline__ void head_freqs(const int8_t* A, int M, int K, const 
         const unsigned Q = R / S;
         L.row_am[lane] = am;
         L.row_Q[lane] = Q;
-        L.row_Rm[lane] = (double)(R - Q * S);
-        L.row_inv[lane] = 1.0 / (double)S;
+        L.row_y[lane] = (double)(R - Q * S) / (double)S;
     }
     __syncthreads();
     // f in place of e
@@ -116,14 +116,14 @@ __device__ __forceinline__ void head_freqs(const int8_t* A, int M, int K, const 
     for (int i = 0; i < 4; i++) {
         const int rr = i * 16 + lr;
         const unsigned Q = L.row_Q[rr];
-        const double Rm = L.row_Rm[rr], inv = L.row_inv[rr];
+        const double y = L.row_y[rr];
 #pragma unroll
         for (int t = 0; t < CT; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const unsigned e = (unsigned)acc[i][t][r];
-                const unsigned q = (unsigned)__builtin_fma((double)e * Rm, inv, 0x1p-30);
-                acc[i][t][r] = (int)(1u + __umul24(e, Q) + q);  // e < 2^16, Q < 2^15
+                const unsigned q1 = (unsigned)__builtin_fma((double)e, y, 1.0 + 0x1p-30);  // 1 + floor(e*Rm/S)
+                acc[i][t][r] = (int)(__umul24(e, Q) + q1);  // e < 2^16, Q < 2^15
             }
     }
 }

@@ -26,18 +26,27 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int rr = i * 16 + lr;
-        const int tok = tokr[i];
-        unsigned fs = 0, lo = 0, ft = 0;
+        // the lane's columns of tile t are nb + 16 t + c4 + (0..3): whole
+        // groups below the target count in full; the group that holds the
+        // target (kt = 16 t + r, r < 4; at most one per lane) gives the
+        // columns before it and f(target)
+        const int kt = tokr[i] - (nb + c4);
+        unsigned fs = 0, lo = 0;
+        v4i grp_t = acc[i][0];
 #pragma unroll
-        for (int t = 0; t < CT; t++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int col = nb + t * 16 + c4 + r;
-                const unsigned f = (unsigned)acc[i][t][r];
-                fs += f;
-                lo += col < tok ? f : 0u;
-                ft += col == tok ? f : 0u;
-            }
+        for (int t = 0; t < CT; t++) {
+            const unsigned p = (unsigned)acc[i][t][0] + (unsigned)acc[i][t][1] + (unsigned)acc[i][t][2] + (unsigned)acc[i][t][3];
+            fs += p;
+            lo += kt >= 16 * t + 4 ? p : 0u;
+            if (t > 0) grp_t = (kt >> 4) == t ? acc[i][t] : grp_t;
+        }
+        const int r = kt & 15;
+        const bool holds = kt >= 0 && kt < 16 * CT && r < 4;
+        const unsigned part = (r > 0 ? (unsigned)grp_t[0] : 0u) + (r > 1 ? (unsigned)grp_t[1] : 0u) +
+                              (r > 2 ? (unsigned)grp_t[2] : 0u);
+        const unsigned fr = r == 0 ? (unsigned)grp_t[0] : r == 1 ? (unsigned)grp_t[1] : r == 2 ? (unsigned)grp_t[2] : (unsigned)grp_t[3];
+        lo += holds ? part : 0u;
+        unsigned ft = holds ? fr : 0u;
         fs += (unsigned)__shfl_xor((int)fs, 16, 64);
         fs += (unsigned)__shfl_xor((int)fs, 32, 64);
         lo += (unsigned)__shfl_xor((int)lo, 16, 64);
