@@ -472,16 +472,19 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
         const unsigned v = row_v[rr], rem = row_rem[rr];
         const int am = L.row_am[rr];
         unsigned run = L.red_c[wave][rr];
+        // the lane's 4-column group of tile t holding v, if any: kept in
+        // registers, one store per row
+        int fsym = -1;
+        unsigned flo = 0u, fhi = 0u;
 #pragma unroll
         for (int t = 0; t < CT; t++) {
-            unsigned g = 0;
+            unsigned f[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int col = nb + t * 16 + c4 + r;
-                const unsigned f = (unsigned)acc[i][t][r] + (col == am ? rem : 0u);
-                acc[i][t][r] = (int)f;
-                g += f;
+                f[r] = (unsigned)acc[i][t][r] + (col == am ? rem : 0u);
             }
+            const unsigned g = f[0] + f[1] + f[2] + f[3];
             // inclusive prefix over the four lane groups of the row, and their total
             unsigned x = g;
             const unsigned y1 = (unsigned)__shfl_up((int)x, 16, 64);
@@ -489,18 +492,19 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
             const unsigned y2 = (unsigned)__shfl_up((int)x, 32, 64);
             x += grp >= 2 ? y2 : 0u;
             const unsigned tile_sum = (unsigned)__shfl((int)x, lr + 48, 64);
-            unsigned lo = run + x - g;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const unsigned hi = lo + (unsigned)acc[i][t][r];
-                if (lo <= v && v < hi) {
-                    row_sym[rr] = nb + t * 16 + c4 + r;
-                    row_lo[rr] = lo;
-                    row_hi[rr] = hi;
-                }
-                lo = hi;
-            }
+            // cumulative bounds of the group's columns: [b0, b1), [b1, b2), ...
+            const unsigned b0 = run + x - g, b1 = b0 + f[0], b2 = b1 + f[1], b3 = b2 + f[2], b4 = b3 + f[3];
+            const unsigned k = (v >= b1 ? 1u : 0u) + (v >= b2 ? 1u : 0u) + (v >= b3 ? 1u : 0u);
+            const bool in = b0 <= v && v < b4;  // every f >= 1: at most one column holds v
+            fsym = in ? nb + t * 16 + c4 + (int)k : fsym;
+            flo = in ? (k == 0 ? b0 : k == 1 ? b1 : k == 2 ? b2 : b3) : flo;
+            fhi = in ? (k == 0 ? b1 : k == 1 ? b2 : k == 2 ? b3 : b4) : fhi;
             run += tile_sum;
+        }
+        if (fsym >= 0) {
+            row_sym[rr] = fsym;
+            row_lo[rr] = flo;
+            row_hi[rr] = fhi;
         }
     }
     __syncthreads();
