@@ -427,30 +427,14 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
     const int b = m0 + lane;
     bool live = false;
     unsigned low = 0, high = 0, code = 0;
-    long long bp = 0, len = 0;
-    int bi = 7;
-    const uint8_t* data = ds.data;
     if (wave == 0 && b < a.M && a.p < ds.ntok[b]) {
         live = true;
         low = st.low[b];
         high = st.high[b];
         code = st.code[b];
-        bp = st.byte_pos[b];
-        bi = st.bit_pos[b];
-        len = ds.blen[b];
-        data += ds.offs[b];
     }
-    // the next 8 bytes of the stream (MSB first from byte bp; zeros past the
-    // end, arith_coder.rs:176-190), requested once the logits are formed so
-    // that they arrive during the reductions
-    unsigned long long win = 0;
     v4i acc[4][CT];
-    head_freqs<CT>(a.A, a.M, a.K, a.W, a.V, m0, a.lut, a.coef, a.total, L, acc, [&] {
-        if (live) {
-#pragma unroll
-            for (int k = 0; k < 8; k++) win |= (unsigned long long)(bp + k < len ? data[bp + k] : 0) << (56 - 8 * k);
-        }
-    });
+    head_freqs<CT>(a.A, a.M, a.K, a.W, a.V, m0, a.lut, a.coef, a.total, L, acc);
     // sum f per row and wave
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -530,6 +514,14 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
     unsigned long long nh = low + udiv64_32((unsigned long long)row_hi[lane] * range, a.total, invT) - 1;
     unsigned long long nl = low + udiv64_32((unsigned long long)row_lo[lane] * range, a.total, invT);
     unsigned long long cd = code;
+    // bits MSB first from byte bp, bit bi on (zeros past the end: arith_coder.rs:176-190)
+    const uint8_t* data = ds.data + ds.offs[b];
+    const long long len = ds.blen[b];
+    const long long bp = st.byte_pos[b];
+    const int bi = st.bit_pos[b];
+    unsigned long long win = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) win |= (unsigned long long)(bp + k < len ? data[bp + k] : 0) << (56 - 8 * k);
     int pos = 56 + bi;  // window bit of the next stream bit
     for (;;) {
         if (((nl ^ nh) & DHALF) == 0) {

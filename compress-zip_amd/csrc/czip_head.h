@@ -34,11 +34,10 @@ struct HeadLds {
 // its error is < 2^16 * 2^-54 + 2^-37 < 2^-36, while a nonzero fraction of
 // e*Rm/S is >= 1/S >= 2^-26 (S < 2^26).  The argmax's remainder
 // (total - sum f) is left to the caller.
-// mid() runs once the logits are formed, before the first reduction.
-template <int CT, class Mid>
+template <int CT>
 __device__ __forceinline__ void head_freqs(const int8_t* A, int M, int K, const int8_t* W, int V, int m0,
                                            const uint16_t* lut, unsigned coef, unsigned total, HeadLds& L,
-                                           v4i (&acc)[4][CT], Mid mid) {
+                                           v4i (&acc)[4][CT]) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nb = wave * CT * 16;
     const int lr = lane & 15, c4 = (lane >> 4) * 4;
@@ -48,7 +47,6 @@ __device__ __forceinline__ void head_freqs(const int8_t* A, int M, int K, const 
 #pragma unroll
         for (int t = 0; t < CT; t++) acc[i][t] = (v4i){0, 0, 0, 0};
     rowblock_mma<CT>(A, M, K, W, V, m0, nb, L.As, acc);
-    mid();
 
     // 1. row max
 #pragma unroll

@@ -22,7 +22,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) tokr[i] = m0 + i * 16 + lr < a.M ? (int)a.targets[m0 + i * 16 + lr] : 0;
     v4i acc[4][CT];
-    head_freqs<CT>(a.A, a.M, a.K, a.W, a.V, m0, a.lut, a.coef, a.total, L, acc, [] {});
+    head_freqs<CT>(a.A, a.M, a.K, a.W, a.V, m0, a.lut, a.coef, a.total, L, acc);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int rr = i * 16 + lr;
