@@ -9,19 +9,21 @@
 // records every weight uses the same max, so a segment's contribution is a
 // plain integer sum (S in u64, vacc modulo 2^32) that can be formed in any
 // order; only the rescales must be applied in key order.  Per tile the wave:
-//  1. forms S^T = K Q^T (int8 MFMA) and the score epilogue in f64, which is
-//     exact: |dot / 4 * mult| < 2^49;
+//  1. forms S^T = K Q^T (int8 MFMA, K rows permuted so that each lane gets
+//     16 consecutive keys of its row) and the score epilogue in f64, which
+//     is exact: |dot / 4 * mult| < 2^49;
 //  2. scans its rows' keys in order (a lane owns 16 consecutive keys of one
 //     row): running max, records, one exp per key.  A key's weight and, at a
 //     record, the rescale factor are both E(-|s - max before the key|);
 //  3. for each segment index j = 0..max records, forms the segment sums of
 //     all 16 rows at once, O_j^T = V^T P_j^T, on int8 MFMA.  The 16-bit
 //     weights enter as two signed bytes: w - 32896 = 256*hi + lo, keys outside
-//     segment j carry w = 0, and the constant 32896 * sum(v) (one more MFMA,
-//     against a column of ones) is added back;
+//     segment j carry w = 0, and the constant 32896 * sum(v) (rows of ones
+//     times V) is added back; each row's weight sum for S comes from rows of
+//     ones times the weight columns;
 //  4. hands O_j through LDS to a "lanes = head dims" layout and walks each
-//     row's own segments: rescale at the record, then add (rows with fewer
-//     records skip the pass with a scalar branch); S is kept with lanes = rows.
+//     row's own segments: rescale at the record, then add (rows without a
+//     segment j skip the pass on a ballot bit); S is kept with lanes = rows.
 // INT32_MIN is the reference's "nothing seen yet" max (the fast path's scores
 // stay inside +-2^30, so no score equals it).
 #pragma once
