@@ -212,18 +212,24 @@ def main():
     if not args.no_decompress:
         ntoks = [min(chunk, n - c * chunk) for c in range(len(chunks))]
         djob = model.decompress_plan(chunks, ntoks)
-        model.reset_stats()
-        model.set_profiling(True)
+        # the rate comes from a run without events (a decode job launches
+        # ~7 kernels per step); the per-kernel times from a second run of the
+        # same job with HIP events around every launch
         t0 = time.perf_counter()
         djob.run()
         t1 = time.perf_counter()
-        model.set_profiling(False)
         back = djob.fetch()
-        djob.free()
         if not np.array_equal(back, tokens):
             raise SystemExit("decompressed tokens differ from the input")
         if text is not None and tokenizer.decode_bytes(back) != text:
             raise SystemExit("detokenized output differs from the input text")
+        model.reset_stats()
+        model.set_profiling(True)
+        djob.run()
+        model.set_profiling(False)
+        if not np.array_equal(djob.fetch(), tokens):
+            raise SystemExit("decompressed tokens differ from the input (profiled run)")
+        djob.free()
         dk = {}
         for name in ["dec_init", "dec_prep", "embed_norm", "qkv_table", "gemm_qkv", "attn_decode", "gemm_o", "gemm_o_norm",
                      "row_norm", "gemm_up", "gemm_down", "gemm_down_norm", "head_dec", "gemm_head", "cdf_decode"]:
