@@ -227,6 +227,8 @@ __global__ __launch_bounds__(256) void k_qkv_table(QkvTabArgs a) {
         return;
     }
     const bool isq = it < 8 * a.H;
+    // Q: >> 15 then NET_SHIFT = 1 (attention.rs:53-83); K: >> 15 (attention.rs:29-50)
+    const double rm = isq ? 0.5 : 1.0, rb = isq ? 3377699720527872.0 : 0.0;
     const int hd = isq ? it >> 3 : (it - 8 * a.H) >> 3, i0 = 4 * (it & 7);
     const int col = isq ? 64 * hd : a.d + 64 * hd;
     const unsigned xw = *(const unsigned*)(t + col + i0), yw = *(const unsigned*)(t + col + i0 + 32);
@@ -239,13 +241,8 @@ __global__ __launch_bounds__(256) void k_qkv_table(QkvTabArgs a) {
         const int c = (int16_t)(r & 1 ? cc >> 16 : cc & 0xFFFFu), sn = (int16_t)(r & 1 ? ss >> 16 : ss & 0xFFFFu);
         const int xr = (int)((unsigned)(xv * c) - (unsigned)(yv * sn));
         const int yr = (int)((unsigned)(xv * sn) + (unsigned)(yv * c));
-        if (isq) {  // attention.rs:53-83 (>>15 then NET_SHIFT=1)
-            xq[r] = clamp127(rne_shr(rne_shr(xr, 15), 1));
-            yq[r] = clamp127(rne_shr(rne_shr(yr, 15), 1));
-        } else {    // attention.rs:29-50
-            xq[r] = clamp127(rne_shr(xr, 15));
-            yq[r] = clamp127(rne_shr(yr, 15));
-        }
+        xq[r] = clamp127(rope_round(xr, rm, rb));
+        yq[r] = clamp127(rope_round(yr, rm, rb));
     }
     int8_t* dst = isq ? a.q8 + (size_t)row * a.d + 64 * hd : a.kc + (((size_t)b * a.KH + hd) * a.T + p) * 64;
     *(unsigned*)(dst + i0) = pack4(xq);
@@ -278,6 +275,8 @@ __global__ __launch_bounds__(256) void k_qkv_table_blk(QkvTabArgs a) {
         const int k = idx / per_row, it = idx - k * per_row;
         const int8_t* t = a.tab + (size_t)tk[k] * a.qkv_n;
         const bool isq = it < 8 * a.H;
+        // Q: >> 15 then NET_SHIFT = 1 (attention.rs:53-83); K: >> 15 (attention.rs:29-50)
+        const double rm = isq ? 0.5 : 1.0, rb = isq ? 3377699720527872.0 : 0.0;
         const int hd = isq ? it >> 3 : (it - 8 * a.H) >> 3, i0 = 4 * (it & 7);
         const int col = isq ? 64 * hd : a.d + 64 * hd;
         const unsigned xw = *(const unsigned*)(t + col + i0), yw = *(const unsigned*)(t + col + i0 + 32);
@@ -291,13 +290,8 @@ __global__ __launch_bounds__(256) void k_qkv_table_blk(QkvTabArgs a) {
             const int c = (int16_t)(r & 1 ? cc >> 16 : cc & 0xFFFFu), sn = (int16_t)(r & 1 ? ss >> 16 : ss & 0xFFFFu);
             const int xr = (int)((unsigned)(xv * c) - (unsigned)(yv * sn));
             const int yr = (int)((unsigned)(xv * sn) + (unsigned)(yv * c));
-            if (isq) {  // attention.rs:53-83 (>>15 then NET_SHIFT=1)
-                xq[r] = clamp127(rne_shr(rne_shr(xr, 15), 1));
-                yq[r] = clamp127(rne_shr(rne_shr(yr, 15), 1));
-            } else {    // attention.rs:29-50
-                xq[r] = clamp127(rne_shr(xr, 15));
-                yq[r] = clamp127(rne_shr(yr, 15));
-            }
+            xq[r] = clamp127(rope_round(xr, rm, rb));
+            yq[r] = clamp127(rope_round(yr, rm, rb));
         }
         int8_t* dst = isq ? qs + k * a.d + 64 * hd : ks + (hd * 16 + k) * 64;
         *(unsigned*)(dst + i0) = pack4(xq);
