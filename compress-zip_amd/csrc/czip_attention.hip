@@ -5,10 +5,12 @@
 namespace czip {
 
 // ---------------------------------------------------------------------------
-// One workgroup = one chunk, one head, 64 query rows (4 waves x 16 rows).  The
-// K / V^T tiles of 64 keys are staged in LDS once for the 4 waves (the next
-// tile is fetched into registers meanwhile); each wave runs attn_tile over
-// its 16 rows.
+// One workgroup = one chunk, one head, 16 * ATT_WAVES query rows (a wave per
+// 16 rows).  The K / V^T tiles of 64 keys are staged in LDS once for the
+// waves (the next tile is fetched into registers meanwhile); each wave runs
+// attn_tile over its 16 rows.  The waves meet at a barrier per tile and their
+// record passes differ, so each waits for the slowest: two waves per
+// workgroup (22.5 KB of LDS, 7 workgroups per CU) lose less there than four.
 // ---------------------------------------------------------------------------
 
 // K and V^T tiles in LDS: row r (64 bytes) of the tile at r * 64, its 16-byte
@@ -19,12 +21,15 @@ namespace czip {
 __device__ __forceinline__ int lds_k(int r, int c) { return r * 64 + ((c ^ ((r >> 4) & 3)) << 4); }
 __device__ __forceinline__ int lds_v(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
 
-template <bool GEN>
-__global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
+constexpr int ATT_WAVES = 2;  // wavefronts (16 query rows each) per workgroup
+
+template <bool GEN, int NWV>
+__global__ __launch_bounds__(64 * NWV, 4) void k_attention(AttnArgs a) {
+    constexpr int QR = 16 * NWV, KPT = 4 / NWV;  // query rows per workgroup; staging loads per thread
     __shared__ unsigned lut32[256];
     __shared__ __attribute__((aligned(16))) int8_t Ks[64 * 64];
     __shared__ __attribute__((aligned(16))) int8_t Vt[64 * 64];
-    __shared__ __attribute__((aligned(16))) AttnWaveLds wl[4];
+    __shared__ __attribute__((aligned(16))) AttnWaveLds wl[NWV];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -32,14 +37,14 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
     // 1-D grid, XCD-aware: workgroups go round-robin over the 8 XCDs; XCD x
     // takes chunks x, x + 8, ..., all (query block, head) pairs of a chunk in a
     // row, so a chunk's K/V tiles are fetched into one L2 only.
-    const int nq = (a.T + 63) / 64, per_chunk = nq * a.H;
+    const int nq = (a.T + QR - 1) / QR, per_chunk = nq * a.H;
     const int xcd = (int)(blockIdx.x % 8u), jx = (int)(blockIdx.x / 8u);
     const int b = (jx / per_chunk) * 8 + xcd;
     if (b >= a.B) return;
-    const int q0 = ((jx % per_chunk) % nq) * 64, h = (jx % per_chunk) / nq;
+    const int q0 = ((jx % per_chunk) % nq) * QR, h = (jx % per_chunk) / nq;
     const int T = a.T, len = a.lens[b];
     if (q0 >= len) return;
-    lut32[tid] = (unsigned)a.lut[tid] << 16;
+    for (int i = tid; i < 256; i += 64 * NWV) lut32[i] = (unsigned)a.lut[i] << 16;
     AttnWaveLds& W = wl[wave];
     const int D = a.H * 64;
     const int g = a.kv_mode == 1 ? (h * a.G) / a.H : 0;
@@ -68,25 +73,37 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
         st.S = 65535u;
     }
 
-    const int ntiles = (min(q0 + 63, len - 1)) / 64 + 1;
-    // K / V^T tile of 64 keys: thread -> row tid/4, 16 bytes; V^T is stored
-    // in blocks of 16 keys ([key/16][dim][16]).  Buffer loads: the tile offset
-    // is uniform, and keys past T read as 0 (the resource's range check).
-    const int ldr = tid >> 2, ldc = (tid & 3) * 16;
+    const int ntiles = (min(q0 + QR - 1, len - 1)) / 64 + 1;
+    // K / V^T tile of 64 keys: 16-byte piece c = tid + 64 NWV n -> row c/4,
+    // chunk c%4; V^T is stored in blocks of 16 keys ([key/16][dim][16]).
+    // Buffer loads: the tile offset is uniform, and keys past T read as 0
+    // (the resource's range check).
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)Kg, (short)0, T * 64, BUF_DWORD3);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)Vg, (short)0, a.TP * 64, BUF_DWORD3);
-    const int koff = ldr * 64 + ldc, voff = (ldc >> 4) * 1024 + ldr * 16;
-    v4i kreg = __builtin_amdgcn_raw_buffer_load_b128(rk, koff, 0, 0);
-    v4i vreg = __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 0, 0);
+    v4i kreg[KPT], vreg[KPT];
+#pragma unroll
+    for (int n = 0; n < KPT; n++) {
+        const int c = tid + 64 * NWV * n, ldr = c >> 2, ldc = (c & 3) * 16;
+        kreg[n] = __builtin_amdgcn_raw_buffer_load_b128(rk, ldr * 64 + ldc, 0, 0);
+        vreg[n] = __builtin_amdgcn_raw_buffer_load_b128(rv, (ldc >> 4) * 1024 + ldr * 16, 0, 0);
+    }
     for (int kt = 0; kt < ntiles; kt++) {
         const int t0 = kt * 64;
         __syncthreads();
-        *(v4i*)(Ks + lds_k(ldr, tid & 3)) = kreg;
-        *(v4i*)(Vt + lds_v(ldr, tid & 3)) = vreg;
+#pragma unroll
+        for (int n = 0; n < KPT; n++) {
+            const int c = tid + 64 * NWV * n;
+            *(v4i*)(Ks + lds_k(c >> 2, c & 3)) = kreg[n];
+            *(v4i*)(Vt + lds_v(c >> 2, c & 3)) = vreg[n];
+        }
         __syncthreads();
         if (kt + 1 < ntiles) {
-            kreg = __builtin_amdgcn_raw_buffer_load_b128(rk, koff, (t0 + 64) * 64, 0);
-            vreg = __builtin_amdgcn_raw_buffer_load_b128(rv, voff, (t0 + 64) * 64, 0);
+#pragma unroll
+            for (int n = 0; n < KPT; n++) {
+                const int c = tid + 64 * NWV * n, ldr = c >> 2, ldc = (c & 3) * 16;
+                kreg[n] = __builtin_amdgcn_raw_buffer_load_b128(rk, ldr * 64 + ldc, (t0 + 64) * 64, 0);
+                vreg[n] = __builtin_amdgcn_raw_buffer_load_b128(rv, (ldc >> 4) * 1024 + ldr * 16, (t0 + 64) * 64, 0);
+            }
         }
         if (!wave_live || t0 > wave_last) continue;
         int nvalid = p - (t0 + grp * 16) + 1;  // keys t <= p are visible (causal)
@@ -111,11 +128,12 @@ __global__ __launch_bounds__(256, 4) void k_attention(AttnArgs a) {
 void launch_attention(const AttnArgs& a, int B, hipStream_t s) {
     AttnArgs g = a;
     g.B = B;
-    dim3 grid((unsigned)(((B + 7) / 8) * 8 * ((a.T + 63) / 64) * a.H));
+    constexpr int NWV = ATT_WAVES;
+    dim3 grid((unsigned)(((B + 7) / 8) * 8 * ((a.T + 16 * NWV - 1) / (16 * NWV)) * a.H));
     if (a.general)
-        hipLaunchKernelGGL(k_attention<true>, grid, dim3(256), 0, s, g);
+        hipLaunchKernelGGL((k_attention<true, NWV>), grid, dim3(64 * NWV), 0, s, g);
     else
-        hipLaunchKernelGGL(k_attention<false>, grid, dim3(256), 0, s, g);
+        hipLaunchKernelGGL((k_attention<false, NWV>), grid, dim3(64 * NWV), 0, s, g);
 }
 
 }  // namespace czip
