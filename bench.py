@@ -27,8 +27,8 @@ PEAK_HBM_GBS = 8000.0       # GB/s
 # HBM bytes per token (read + write) of each kernel on the text workload, from
 # two rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0: the factors a
 # plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text_1Mtok.md
-TRAFFIC_B_PER_TOKEN = {"attention": 514 + 384, "qkv_table": 12 + 512, "gemm_o_norm": 397 + 1152,
-                       "gemm_down_norm": 1820 + 384, "gemm_up": 552 + 1024, "head_cdf": 391 + 8}
+TRAFFIC_B_PER_TOKEN = {"attention": 523 + 405, "qkv_table": 13 + 512, "gemm_o_norm": 397 + 1152,
+                       "gemm_down_norm": 1814 + 384, "gemm_up": 556 + 1024, "head_cdf": 391 + 8}
 TRAFFIC_WORKLOADS = ("v001_L4_ctx512_text64MiB",)
 
 WORKLOADS = {
