@@ -90,6 +90,7 @@ struct czip_ctx {
     };
     std::vector<Pending> pending;
     std::vector<hipEvent_t> event_pool;
+    czip_job* dec = nullptr;  // step-wise decode session (czip_decode_begin)
 };
 
 struct czip_job {
@@ -120,6 +121,9 @@ struct czip_job {
     int64_t *d_offs = nullptr, *d_toff = nullptr, *st_bpos = nullptr;
     int32_t *d_blen = nullptr, *d_ntok = nullptr, *st_bit = nullptr;
     uint32_t *d_tokens = nullptr, *st_low = nullptr, *st_high = nullptr, *st_code = nullptr;
+    // step-wise decode session
+    uint32_t *d_val = nullptr, *d_out = nullptr;
+    std::vector<int32_t> h_lens;
 };
 
 namespace {
@@ -366,10 +370,13 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
     return CZIP_OK;
 }
 
+static void free_decode_session(czip_ctx* c);
+
 extern "C" void czip_destroy(czip_ctx* c) {
     if (!c) return;
     hipSetDevice(c->device);
     if (c->stream) hipStreamSynchronize(c->stream);
+    free_decode_session(c);
     for (auto& p : c->pending) { hipEventDestroy(p.a); hipEventDestroy(p.b); }
     for (auto e : c->event_pool) hipEventDestroy(e);
     for (void* p : c->allocs) hipFree(p);
@@ -925,4 +932,136 @@ extern "C" void czip_job_free(czip_job* j) {
     hipStreamSynchronize(j->ctx->stream);
     free_job_mem(j);
     delete j;
+}
+
+// ===========================================================================
+// Step-wise decode: the caller keeps its own arithmetic decoder and drives
+// the per-token loop of main.rs:381-391 for S streams at a time.
+// ===========================================================================
+static void free_decode_session(czip_ctx* c) {
+    if (!c || !c->dec) return;
+    free_job_mem(c->dec);
+    delete c->dec;
+    c->dec = nullptr;
+}
+
+extern "C" czip_status czip_decode_begin(czip_ctx* c, int32_t S, int32_t T) {
+    if (!c) return CZIP_E_ARG;
+    if (S < 1 || T < 1) return fail(c, CZIP_E_ARG, "S and T must be >= 1");
+    if (T > c->cfg.context_length || T > c->cfg.max_seq_len)
+        return fail(c, CZIP_E_RANGE, "T exceeds the RoPE LUT / KV cache (lut.rs:169-177)");
+    HIPCHECK(c, hipSetDevice(c->device));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
+    free_decode_session(c);
+    auto j = std::make_unique<czip_job>();
+    j->ctx = c;
+    j->kind = 2;
+    j->S = S;
+    j->T = T;
+    const size_t d = (size_t)c->cfg.d_model, L = (size_t)c->cfg.n_layers, V = (size_t)c->cfg.vocab;
+    const size_t kv = L * (size_t)S * c->KH * pad64(T) * 64;
+    auto& A = j->allocs;
+    czip_status rc;
+    if ((rc = dalloc(c, A, &j->inp, (size_t)S)) || (rc = dalloc(c, A, &j->d_ntok, (size_t)S)) ||
+        (rc = dalloc(c, A, &j->d_val, (size_t)S)) || (rc = dalloc(c, A, &j->d_out, (size_t)S * std::max<size_t>(V, 3))) ||
+        (rc = dalloc(c, A, &j->x, (size_t)S * d)) || (rc = dalloc(c, A, &j->xn, (size_t)S * d)) ||
+        (rc = dalloc(c, A, &j->q8, (size_t)S * d)) || (rc = dalloc(c, A, &j->attn, (size_t)S * d)) ||
+        (rc = dalloc(c, A, &j->y8, (size_t)S * d)) || (rc = dalloc(c, A, &j->r8, (size_t)S * c->cfg.d_ff)) ||
+        (rc = dalloc(c, A, &j->logits, (size_t)S * V)) ||
+        (rc = dalloc(c, A, &j->rn_ws, std::max<size_t>(gemm_rn_ws_bytes(S, (int)d) / 4, 1))) ||
+        (rc = dalloc(c, A, &j->kc, kv)) || (rc = dalloc(c, A, &j->vc, kv))) {
+        free_job_mem(j.get());
+        return rc;
+    }
+    j->rn_ws_bytes = gemm_rn_ws_bytes(S, (int)d);
+    j->h_lens.assign((size_t)S, -1);
+    c->dec = j.release();
+    return CZIP_OK;
+}
+
+extern "C" czip_status czip_decode_step(czip_ctx* c, const uint32_t* tok_in, const int32_t* pos,
+                                        const uint32_t* value_or_null, uint32_t* out) {
+    if (!c) return CZIP_E_ARG;
+    czip_job* j = c->dec;
+    if (!j) return fail(c, CZIP_E_ARG, "no decode session (czip_decode_begin)");
+    if (!tok_in || !pos || !out) return fail(c, CZIP_E_ARG, "null argument");
+    const int S = j->S, V = c->cfg.vocab, d = c->cfg.d_model;
+    const size_t orow = value_or_null ? 3 : (size_t)V;
+    int p = -1;
+    for (int i = 0; i < S; i++) {
+        if (pos[i] < -1) return fail(c, CZIP_E_ARG, "pos[s] must be a position or -1");
+        if (pos[i] >= 0 && p >= 0 && pos[i] != p)
+            return fail(c, CZIP_E_ARG, "every active stream must be at the same position");
+        if (pos[i] >= 0) p = pos[i];
+    }
+    if (p < 0) {
+        memset(out, 0, (size_t)S * orow * 4);
+        return CZIP_OK;
+    }
+    if (p >= j->T) return fail(c, CZIP_E_RANGE, "position past the session's T (lut.rs:169-177)");
+    for (int i = 0; i < S; i++)
+        if (pos[i] >= 0 && tok_in[i] >= (uint32_t)V)
+            return fail(c, CZIP_E_TOKEN, "token id >= vocab at stream " + std::to_string(i));
+    HIPCHECK(c, hipSetDevice(c->device));
+    hipStream_t s = c->stream;
+    // inactive streams (pos -1) attend to nothing and read token 0; their rows are zeroed below
+    std::vector<uint32_t> tin((size_t)S);
+    bool lens_changed = false;
+    for (int i = 0; i < S; i++) {
+        tin[(size_t)i] = pos[i] >= 0 ? tok_in[i] : 0u;
+        const int32_t l = pos[i] >= 0 ? j->T : 0;
+        lens_changed |= j->h_lens[(size_t)i] != l;
+        j->h_lens[(size_t)i] = l;
+    }
+    HIPCHECK(c, hipMemcpyAsync(j->inp, tin.data(), (size_t)S * 4, hipMemcpyHostToDevice, s));
+    if (lens_changed) HIPCHECK(c, hipMemcpyAsync(j->d_ntok, j->h_lens.data(), (size_t)S * 4, hipMemcpyHostToDevice, s));
+    if (value_or_null) HIPCHECK(c, hipMemcpyAsync(j->d_val, value_or_null, (size_t)S * 4, hipMemcpyHostToDevice, s));
+    const int TP = pad64(j->T);
+    const size_t layer_kv = (size_t)S * c->KH * TP * 64;
+    if (!c->rn_fused) { Timed t(c, "embed_norm"); launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, S, d, j->x, j->xn, s); }
+    for (int l = 0; l < c->cfg.n_layers; l++) {
+        const DevLayer& L = c->layers[(size_t)l];
+        int8_t* kc = j->kc + (size_t)l * layer_kv;
+        int8_t* vc = j->vc + (size_t)l * layer_kv;
+        GemmArgs g{};
+        g.A = j->xn; g.W = L.qkv_w; g.M = S; g.N = L.qkv_n; g.K = d;
+        g.out8 = j->q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
+        g.d = d; g.T = TP; g.TP = TP; g.pos = p; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
+        g.KH = c->KH; g.kc = kc; g.vc = vc; g.rcos = c->rcos; g.rsin = c->rsin;
+        if (l == 0) {
+            layer0_qkv(c, g, j->inp, s);
+        } else {
+            Timed t(c, "gemm_qkv");
+            launch_gemm(g, EPI_QKV, s);
+        }
+        AttnArgs a{};
+        a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = j->d_ntok; a.score_mult = L.score_mult;
+        a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = S; a.T = TP; a.H = c->cfg.n_heads; a.G = c->cfg.n_kv_heads;
+        a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
+        a.general = L.attn_general;
+        { Timed t(c, "attn_decode"); launch_attn_decode(a, S, p, s); }
+        post_attention(c, j, l, S);
+    }
+    {
+        GemmArgs hd{};
+        hd.A = j->xn; hd.W = c->head_w; hd.M = S; hd.N = V; hd.K = d; hd.out32 = j->logits; hd.ldo = V;
+        { Timed t(c, "gemm_head"); launch_gemm(hd, EPI_RAW, s); }
+        Timed t(c, "cdf");
+        launch_cdf(j->logits, S, V, value_or_null ? j->d_val : nullptr, nullptr, 1, c->lut, c->cfg.coef_q24,
+                   c->cfg.target_total, value_or_null ? 2 : 1, j->d_out, 0, s);
+    }
+    HIPCHECK(c, hipGetLastError());
+    HIPCHECK(c, hipMemcpyAsync(out, j->d_out, (size_t)S * orow * 4, hipMemcpyDeviceToHost, s));
+    HIPCHECK(c, hipStreamSynchronize(s));
+    resolve_events(c);
+    for (int i = 0; i < S; i++)
+        if (pos[i] < 0) memset(out + (size_t)i * orow, 0, orow * 4);
+    return CZIP_OK;
+}
+
+extern "C" void czip_decode_end(czip_ctx* c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+    free_decode_session(c);
 }

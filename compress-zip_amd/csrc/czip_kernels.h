@@ -123,8 +123,9 @@ void launch_resid_norm(int16_t* x, const int8_t* y8, const int8_t* w1, const int
                        int8_t* xn, hipStream_t s);
 void launch_gemm(const GemmArgs& a, int epi, hipStream_t s);
 void launch_attention(const AttnArgs& a, int B, hipStream_t s);
-// mode 0: (lo, hi) of targets; mode 1: full inclusive cumfreqs.  Row r of
-// the launch is written at output row out_row0 + r.
+// mode 0: (lo, hi) of targets; mode 1: full inclusive cumfreqs; mode 2:
+// targets are decoder values, out rows (sym, cum_lo, cum_hi).  Row r of the
+// launch is written at output row out_row0 + r.
 void launch_cdf(const int32_t* logits, int M, int V, const uint32_t* targets, const int32_t* lens, int T,
                 const uint16_t* lut, unsigned coef, unsigned total, int mode, uint32_t* out, int64_t out_row0,
                 hipStream_t s);

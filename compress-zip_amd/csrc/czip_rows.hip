@@ -389,7 +389,11 @@ void launch_resid_norm(int16_t* x, const int8_t* y8, const int8_t* w1, const int
 // because S >= 65535 (the max logit weighs 65535), and the small quotient is
 // an f32 estimate corrected by one exact 64-bit remainder test.
 // mode 0: write (cum_lo, cum_hi) of the row's target; mode 1: write the full
-// inclusive table.
+// inclusive table; mode 2: targets holds the row's decoder value (the
+// ((code - low + 1) * total - 1) / range of arith_coder.rs:199-203) and the
+// row gets (sym, cum_lo, cum_hi) with sym the first index whose inclusive
+// cumulative frequency exceeds the value, clamped to V - 1
+// (bisect_cumfreqs, arith_coder.rs:225-241).
 // ---------------------------------------------------------------------------
 template <int WPR, int EPL>
 __global__ __launch_bounds__(64 * WPR) void k_cdf(const int32_t* __restrict__ logits, int V,
@@ -513,12 +517,38 @@ __global__ __launch_bounds__(64 * WPR) void k_cdf(const int32_t* __restrict__ lo
             for (int w = 0; w < wave; w++) excl += red_u[w];
         }
         unsigned run = excl + (am < i0 ? rem : 0u);
-        uint32_t* o = out + (size_t)(out_row0 + row) * V;
+        if (mode == 1) {
+            uint32_t* o = out + (size_t)(out_row0 + row) * V;
 #pragma unroll
-        for (int k = 0; k < EPL; k++) {
-            if (i0 + k < V) {
-                run += e[k] + (i0 + k == am ? rem : 0u);
-                o[i0 + k] = run;
+            for (int k = 0; k < EPL; k++) {
+                if (i0 + k < V) {
+                    run += e[k] + (i0 + k == am ? rem : 0u);
+                    o[i0 + k] = run;
+                }
+            }
+        } else {
+            const unsigned value = targets[row];
+            int cand = 0x7FFFFFFF;
+            unsigned clo = 0, chi = 0;
+#pragma unroll
+            for (int k = 0; k < EPL; k++) {
+                if (i0 + k < V) {
+                    const unsigned before = run;
+                    run += e[k] + (i0 + k == am ? rem : 0u);
+                    // the last symbol also takes a value at or past the total (the clamp)
+                    if (cand == 0x7FFFFFFF && (value < run || i0 + k == V - 1)) {
+                        cand = i0 + k;
+                        clo = before;
+                        chi = run;
+                    }
+                }
+            }
+            const int sym = bmin(cand);
+            if (cand == sym) {
+                uint32_t* o = out + (size_t)(out_row0 + row) * 3;
+                o[0] = (uint32_t)sym;
+                o[1] = clo;
+                o[2] = chi;
             }
         }
     }

@@ -6,6 +6,7 @@
 // and the per-scalar defaults model.rs:157-168.
 #include <cstdio>
 #include <cstdlib>
+#include <cstdint>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -84,10 +85,22 @@ czip_status load_czm(const char* path, int32_t kv_mode, HostModel& hm, std::stri
         if (!ok) { err = "Unknown dtype: " + dt->str; return CZIP_E_IO; }
         HostTensor t;
         t.dtype = dt->str;
+        // shapes and offsets are usize in the reference's header type
+        // (safetensors.rs:287-376): non-negative integers, checked without wrap
+        auto is_usize = [](const JVal& j) { return j.kind == JVal::NUM && j.isint && j.inum >= 0; };
         size_t numel = 1;
-        for (auto& d : sh->arr) { t.shape.push_back(d.inum); numel *= (size_t)d.inum; }
-        size_t a = (size_t)off->arr[0].inum, b = (size_t)off->arr[1].inum;
-        if (b < a || base + b > (size_t)sz || b - a != numel * es) { err = "bad data_offsets for " + kv.first; return CZIP_E_IO; }
+        for (auto& d : sh->arr) {
+            if (!is_usize(d)) { err = "bad shape for " + kv.first; return CZIP_E_IO; }
+            t.shape.push_back(d.inum);
+            if (d.inum != 0 && numel > SIZE_MAX / (size_t)d.inum) { err = "shape overflow for " + kv.first; return CZIP_E_IO; }
+            numel *= (size_t)d.inum;
+        }
+        if (!is_usize(off->arr[0]) || !is_usize(off->arr[1])) { err = "bad data_offsets for " + kv.first; return CZIP_E_IO; }
+        const size_t a = (size_t)off->arr[0].inum, b = (size_t)off->arr[1].inum, blob = (size_t)sz - base;
+        if (numel > SIZE_MAX / es || b < a || b > blob || b - a != numel * es) {
+            err = "bad data_offsets for " + kv.first;
+            return CZIP_E_IO;
+        }
         t.data = hm.blob.data() + base + a;
         t.bytes = b - a;
         t.numel = numel;

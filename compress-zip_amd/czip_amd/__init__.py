@@ -93,6 +93,9 @@ SIGNATURES = {
     "czip_chunk_slot_bytes": (C.c_int64, [C.c_int32]),
     "czip_decompress_plan": (C.c_int32, [_P, _P, _P, _P, _P, C.c_int32, C.POINTER(C.c_void_p)]),
     "czip_decompress_fetch": (C.c_int32, [_P, _P, _P]),
+    "czip_decode_begin": (C.c_int32, [_P, C.c_int32, C.c_int32]),
+    "czip_decode_step": (C.c_int32, [_P, _P, _P, _P, _P]),
+    "czip_decode_end": (None, [_P]),
     "czip_tokenizer_load": (C.c_int32, [C.c_char_p, C.c_size_t, C.POINTER(C.c_void_p)]),
     "czip_tokenizer_from_model": (C.c_int32, [_P, C.POINTER(C.c_void_p)]),
     "czip_tokenizer_free": (None, [_P]),
@@ -300,6 +303,32 @@ class Model:
             return job.fetch()
         finally:
             job.free()
+
+    # --- step-wise decode (the caller keeps the arithmetic decoder) ---
+    def decode_begin(self, S: int, T: int):
+        """Open the decode session of S streams of at most T tokens."""
+        self._check(lib().czip_decode_begin(self._ctx, S, T))
+        self._dec_S = S
+
+    def decode_step(self, tok_in, pos, values=None) -> np.ndarray:
+        """forward + cumfreqs of every stream at its position (-1: inactive);
+        with `values` (the decoders' targets) returns [S, 3] (sym, cum_lo,
+        cum_hi), else the [S, V] cumulative tables."""
+        S = self._dec_S
+        tok_in = np.ascontiguousarray(tok_in, dtype=np.uint32).reshape(S)
+        pos = np.ascontiguousarray(pos, dtype=np.int32).reshape(S)
+        if values is None:
+            out = np.zeros((S, self.vocab), np.uint32)
+            vp = None
+        else:
+            values = np.ascontiguousarray(values, dtype=np.uint32).reshape(S)
+            out = np.zeros((S, 3), np.uint32)
+            vp = _p(values)
+        self._check(lib().czip_decode_step(self._ctx, _p(tok_in), _p(pos), vp, _p(out)))
+        return out
+
+    def decode_end(self):
+        lib().czip_decode_end(self._ctx)
 
     # --- instrumentation ---
     def set_profiling(self, on: bool):

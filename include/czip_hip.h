@@ -140,6 +140,37 @@ czip_status czip_decompress_plan(czip_ctx* ctx, const uint8_t* data, const int64
                                  czip_job** job);
 czip_status czip_decompress_fetch(czip_job* job, uint32_t* tokens_out, const int64_t* tok_offs);
 
+/* ---- step-wise decode, for a caller that keeps its own ArithDecoder
+ *      (arith_coder.rs:139-264): one call replaces, for S streams at once,
+ *      the body of the per-token loop of main.rs:381-391,
+ *        logits = model.forward(prev_token, pos);            (model.rs:362-480)
+ *        cumfreqs = model.get_cumfreqs(&logits);             (model.rs:483-486)
+ *        token = decoder.decode_symbol(&cumfreqs);           (arith_coder.rs:195-222)
+ *      up to the decoder's own interval update and renormalisation.
+ *      czip_decode_begin replaces Model::new + reset per stream (model.rs:315-357):
+ *      it opens the context's decode session for S streams of at most T tokens
+ *      (a KV cache per stream; an open session is replaced).
+ *      czip_decode_step runs forward at position pos[s] on token tok_in[s] for
+ *      every stream s (the BOS 1022 at position 0, main.rs:387).  Every active
+ *      stream must be at the same position p (streams advance in lockstep; a new
+ *      chunk restarts all of them at 0); pos[s] = -1 marks a stream with nothing
+ *      to decode, whose output row is zero.
+ *        value_or_null == NULL: out is [S, V], the inclusive cumulative
+ *          frequencies get_cumfreqs returns (softmax_cdf.rs:85-139);
+ *        else value_or_null[s] is the stream's decoder value
+ *          ((code - low + 1) * total - 1) / range (arith_coder.rs:199-203) and
+ *          out is [S, 3] = (symbol, cum_lo, cum_hi): the first symbol whose
+ *          cumulative frequency exceeds the value, clamped to V - 1
+ *          (bisect_cumfreqs, arith_coder.rs:225-241), cum_lo = cumfreqs[sym-1]
+ *          (0 for sym 0) and cum_hi = cumfreqs[sym]; the caller then narrows and
+ *          renormalises its decoder (arith_coder.rs:212-219) and feeds the
+ *          symbol back as the next tok_in.
+ *      czip_decode_end releases the session (czip_destroy does too). ---- */
+czip_status czip_decode_begin(czip_ctx* ctx, int32_t S, int32_t T);
+czip_status czip_decode_step(czip_ctx* ctx, const uint32_t* tok_in, const int32_t* pos,
+                             const uint32_t* value_or_null, uint32_t* out);
+void        czip_decode_end(czip_ctx* ctx);
+
 /* ---- tokenizer (host): the BPE of the text configurations.
  *      czip_tokenizer_load replaces load_tiktoken_json_from_bytes
  *      (rust/src/tiktoken.rs:536-563); czip_tokenizer_from_model decompresses

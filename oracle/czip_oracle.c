@@ -376,11 +376,19 @@ void orc_state_free(orc_state* s) {
     free(s->dn32); free(s->dn8); free(s);
 }
 
+/* Number of vacc additions whose exact sum left the i32 range (and so
+ * wrapped, as a Rust --release build does), over every attend_head call of
+ * the process.  Instrumentation for the tests; not part of the algorithm. */
+static int64_t g_vacc_wraps = 0;
+int64_t orc_vacc_wraps(void) { return __atomic_load_n(&g_vacc_wraps, __ATOMIC_RELAXED); }
+void orc_vacc_wraps_reset(void) { __atomic_store_n(&g_vacc_wraps, 0, __ATOMIC_RELAXED); }
+
 /* Online-softmax attention of one query head over cache rows 0..=step
  * (attention.rs:197-285).  q is already rotated. */
 static void attend_head(const int8_t* q_rot, const int8_t* kc, const int8_t* vc, int stride,
                         int step, int32_t mult, const int8_t* sink, const uint16_t* lut,
-                        uint32_t coef, int8_t* out) {
+                        uint32_t coef, int8_t* out, int32_t* vacc_out, uint64_t* s_out) {
+    int64_t wraps = 0;
     int32_t m = INT32_MIN;
     uint64_t S = 0;
     int32_t vacc[HEAD_DIM];
@@ -412,10 +420,22 @@ static void attend_head(const int8_t* q_rot, const int8_t* kc, const int8_t* vc,
         uint16_t w = orc_exp_q16_coef(wsub32(score, m), lut, coef);
         S += w;
         const int8_t* v = vc + (size_t)t * stride;
-        for (int i = 0; i < HEAD_DIM; i++) vacc[i] = wadd32(vacc[i], (int32_t)w * (int32_t)v[i]);
+        for (int i = 0; i < HEAD_DIM; i++) {
+            int64_t exact = (int64_t)vacc[i] + (int64_t)w * (int64_t)v[i];
+            vacc[i] = wadd32(vacc[i], (int32_t)w * (int32_t)v[i]);
+            wraps += exact != (int64_t)vacc[i];
+        }
     }
     uint64_t den = S == 0 ? 1 : S;
     for (int i = 0; i < HEAD_DIM; i++) out[i] = orc_clamp_i8(orc_div_rne_s32_by_u64(vacc[i], den));
+    if (vacc_out) memcpy(vacc_out, vacc, sizeof(vacc));
+    if (s_out) *s_out = S;
+    if (wraps) __atomic_add_fetch(&g_vacc_wraps, wraps, __ATOMIC_RELAXED);
+}
+
+void orc_attend_head(const int8_t* q_rot, const int8_t* k, const int8_t* v, int n_keys, int32_t score_mult,
+                     const int8_t* sink, const uint16_t* lut, int8_t* out, int32_t* vacc_out, uint64_t* s_out) {
+    attend_head(q_rot, k, v, HEAD_DIM, n_keys - 1, score_mult, sink, lut, orc_attn_coef_q24(), out, vacc_out, s_out);
 }
 
 int orc_forward(orc_state* s, uint32_t token, int pos, int32_t* logits) {
@@ -466,7 +486,7 @@ int orc_forward(orc_state* s, uint32_t token, int pos, int32_t* logits) {
             orc_rope_q(qr, cs, sn);
             int g = (m->kv_mode == ORC_KV_GQA) ? (h * G) / H : 0;
             attend_head(qr, kc + g * HEAD_DIM, vc + g * HEAD_DIM, kstride, pos, L->score_mult[h],
-                        L->sink_key, m->exp2_lut, acoef, s->attn + h * HEAD_DIM);
+                        L->sink_key, m->exp2_lut, acoef, s->attn + h * HEAD_DIM, NULL, NULL);
         }
         orc_linear_i8_to_i32(s->attn, L->out_w, 1, d, d, s->o32);             /* model.rs:424-425 */
         orc_requant(s->o32, d, L->out_mult, (int8_t)L->out_shift, s->o8);

@@ -49,6 +49,16 @@ void     orc_reglu(const int8_t* x, int d_ff, int8_t* out);
 void     orc_rope_k(int8_t* x64, const int16_t* cos_row, const int16_t* sin_row);
 void     orc_rope_q(int8_t* x64, const int16_t* cos_row, const int16_t* sin_row);
 
+/* One query head's attention over keys 0..n_keys-1 (attention.rs:197-285):
+ * q_rot already rotated, k/v [n_keys, 64] rows, ATTN_COEF_Q24 exp.  The final
+ * i32 vacc and u64 S go to vacc_out/s_out when not NULL. */
+void     orc_attend_head(const int8_t* q_rot, const int8_t* k, const int8_t* v, int n_keys, int32_t score_mult,
+                         const int8_t* sink, const uint16_t* lut, int8_t* out, int32_t* vacc_out, uint64_t* s_out);
+/* Count of vacc additions that wrapped the i32 range since the last reset
+ * (instrumentation: every attention row of orc_forward and orc_attend_head). */
+int64_t  orc_vacc_wraps(void);
+void     orc_vacc_wraps_reset(void);
+
 /* ---- softmax -> cumulative frequencies (softmax_cdf.rs:85-139) ---- */
 void     orc_build_cumfreqs(const int32_t* logits, int v, const uint16_t* lut, uint32_t coef_q24,
                             uint32_t target_total, uint32_t* cum_out);

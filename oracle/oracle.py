@@ -132,6 +132,10 @@ def load(path: str):
     L.orc_reglu.restype = None; L.orc_reglu.argtypes = [p, C.c_int, p]
     L.orc_rope_k.restype = None; L.orc_rope_k.argtypes = [p, p, p]
     L.orc_rope_q.restype = None; L.orc_rope_q.argtypes = [p, p, p]
+    L.orc_attend_head.restype = None
+    L.orc_attend_head.argtypes = [p, p, p, C.c_int, C.c_int32, p, p, p, p, p]
+    L.orc_vacc_wraps.restype = C.c_int64; L.orc_vacc_wraps.argtypes = []
+    L.orc_vacc_wraps_reset.restype = None; L.orc_vacc_wraps_reset.argtypes = []
     L.orc_build_cumfreqs.restype = None
     L.orc_build_cumfreqs.argtypes = [p, C.c_int, p, C.c_uint32, C.c_uint32, p]
     L.orc_model_check.restype = C.c_int; L.orc_model_check.argtypes = [C.POINTER(OrcModel)]
@@ -177,6 +181,33 @@ def decode_symbols(data: bytes, cum: np.ndarray, n: int):
     d = OrcDecoder()
     L.orc_dec_init(C.byref(d), C.cast(buf, C.c_void_p), len(data))
     return [L.orc_dec_decode(C.byref(d), _ptr(cum), cum.size) for _ in range(n)]
+
+
+def attend_head(q_rot: np.ndarray, k: np.ndarray, v: np.ndarray, score_mult: int, lut: np.ndarray, sink=None):
+    """One query head over keys 0..n-1 (attention.rs:197-285): returns
+    (out int8 [64], final i32 vacc [64], final u64 S)."""
+    L = lib()
+    q_rot = np.ascontiguousarray(q_rot, dtype=np.int8)
+    k = np.ascontiguousarray(k, dtype=np.int8)
+    v = np.ascontiguousarray(v, dtype=np.int8)
+    lut = np.ascontiguousarray(lut, dtype=np.uint16)
+    assert q_rot.shape == (64,) and k.ndim == 2 and k.shape[1] == 64 and v.shape == k.shape
+    sk = None if sink is None else np.ascontiguousarray(sink, dtype=np.int8)
+    out = np.zeros(64, np.int8)
+    vacc = np.zeros(64, np.int32)
+    S = C.c_uint64(0)
+    L.orc_attend_head(_ptr(q_rot), _ptr(k), _ptr(v), k.shape[0], int(score_mult),
+                      None if sk is None else _ptr(sk), _ptr(lut), _ptr(out), _ptr(vacc), C.byref(S))
+    return out, vacc, S.value
+
+
+def vacc_wraps() -> int:
+    """vacc additions that wrapped the i32 range since the last reset_vacc_wraps()."""
+    return int(lib().orc_vacc_wraps())
+
+
+def reset_vacc_wraps():
+    lib().orc_vacc_wraps_reset()
 
 
 def _ptr(a: np.ndarray) -> int:

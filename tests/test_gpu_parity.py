@@ -416,3 +416,29 @@ def test_error_codes(gpu_shipped, amd):
         gpu_shipped.compress_plan(np.array([1, 2, 5000], np.uint32), 64)
     assert e.value.code == -5
     assert gpu_shipped.compress_chunks(np.zeros(0, np.uint32), 64) == []
+
+
+def test_vacc_wrap(amd, orc, tmp_path):
+    """Attention sums that wrap the reference's i32 vacc (attention.rs:207-208,
+    274: 65535 * 127 * (p + 1) >= 2^31 from position 258 on): prefill logits
+    of a 512-token chunk, coded bytes of a full and a ragged chunk, and device
+    decode of the oracle's chunks, all against the oracle, whose own sums are
+    checked to have wrapped."""
+    from conftest import write_vacc_wrap_model
+    from czip_amd import synth
+    path = write_vacc_wrap_model(str(tmp_path / "wrap.czm"))
+    gm, om = _model_pair(amd, orc, path, amd.KV_RUST_COMPAT)
+    toks = synth.zipf_ids(512 + 300, 1024, seed=112)
+    inp, _ = _chunk_inputs(toks, [512, 300], 512)
+    _say("vacc wrap: logits of 512 + 300 rows")
+    orc.reset_vacc_wraps()
+    got = gm.forward_logits(inp, [512, 300])
+    for b, n in enumerate([512, 300]):
+        ref, _ = om.trace(inp[b, :n])
+        bad = np.argwhere(got[b, :n] != ref)
+        assert bad.size == 0, f"chunk {b}: first mismatch at (pos, vocab) {bad[0].tolist()}"
+    assert orc.vacc_wraps() > 0
+    _say("vacc wrap: compress + decode")
+    ref = om.compress_many(toks, 512, threads=2)
+    assert gm.compress_chunks(toks, 512) == ref
+    assert np.array_equal(gm.decompress_chunks(ref, [512, 300]), toks)

@@ -61,6 +61,55 @@ def test_loader_errors(tmp_path):
     assert e.value.code == -9          # "Missing tensor" (model.rs:152-154)
 
 
+def _patch_header(src: str, dst: str, edit):
+    """Rewrite the JSON header of a .czm file (same blob after it)."""
+    import json
+    import struct
+    blob = open(src, "rb").read()
+    (hlen,) = struct.unpack("<Q", blob[:8])
+    hdr = json.loads(blob[8:8 + hlen])
+    edit(hdr)
+    hj = json.dumps(hdr).encode()
+    hj += b" " * ((8 - len(hj) % 8) % 8)
+    open(dst, "wb").write(struct.pack("<Q", len(hj)) + hj + blob[8 + hlen:])
+
+
+@pytest.mark.parametrize("bad", ["neg_offset", "str_offset", "float_offset", "neg_dim", "huge_dim", "past_end",
+                                 "swapped"])
+def test_loader_rejects_malformed_offsets(tmp_path, bad):
+    """data_offsets and shape entries must be non-negative integers inside
+    the file (usize in safetensors.rs:287-376): a crafted header gives
+    CZIP_E_IO instead of a tensor pointing outside the blob."""
+    import czip_amd
+    from czip_amd import synth
+    good = synth.write_random_model(str(tmp_path / "good.czm"), d=256, n_layers=1, n_heads=4, n_kv=1, d_ff=256,
+                                    vocab=256, ctx=64)
+    czip_amd.ModelWeights(good)
+
+    def edit(h):
+        e = h["embed.weight"]
+        a, b = e["data_offsets"]
+        if bad == "neg_offset":
+            e["data_offsets"] = [a - (1 << 40), b - (1 << 40)]
+        elif bad == "str_offset":
+            e["data_offsets"] = [str(a), b]
+        elif bad == "float_offset":
+            e["data_offsets"] = [float(a), float(b)]
+        elif bad == "neg_dim":
+            e["shape"] = [-e["shape"][0], -e["shape"][1]]
+        elif bad == "huge_dim":
+            e["shape"] = [1 << 62, 1 << 62]
+        elif bad == "past_end":
+            e["data_offsets"] = [a + (1 << 30), b + (1 << 30)]
+        else:
+            e["data_offsets"] = [b, a]
+    p = str(tmp_path / f"{bad}.czm")
+    _patch_header(good, p, edit)
+    with pytest.raises(czip_amd.CzipError) as e:
+        czip_amd.ModelWeights(p)
+    assert e.value.code == -8
+
+
 def test_random_model_roundtrip(tmp_path, orc):
     import czip_amd
     from czip_amd import synth

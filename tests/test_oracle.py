@@ -334,16 +334,6 @@ def test_coder_random_distributions(orc):
         assert orc.decode_symbols(data, cum, len(syms)) == syms
 
 
-def test_attention_first_position_is_value(orc):
-    """At position 0 a head sees one key: w = E(0) = 65535 = S, so the output
-    is RNE(65535*v/65535) = v (attention.rs:266-283)."""
-    m = orc.Model.from_file(MODEL_PATH)
-    # forward at pos 0 twice with the same token gives identical logits
-    lg1 = m.trace(np.array([5], np.uint32), with_cum=False)
-    lg2 = m.trace(np.array([5], np.uint32), with_cum=False)
-    assert np.array_equal(lg1, lg2)
-
-
 def test_chunk_roundtrip_shipped(orc, shipped):
     rng = np.random.default_rng(8)
     toks = rng.integers(0, 1024, 200).astype(np.uint32)
