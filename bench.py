@@ -82,8 +82,20 @@ def gemm_ops_per_token(cfg, kv_mode):
     return out
 
 
-def cpu_baseline(model_path, tokens, chunk, budget_s=15.0, kv_mode=0):
-    """Oracle (C restatement of the Rust chunk loop) on the host cores."""
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(model_path, tokens, chunk, budget_s=15.0, kv_mode=0, extra_chunks=()):
+    """Oracle (C restatement of the Rust chunk loop) on the host cores.
+    Returns (baseline record, {chunk index: oracle bytes}) for the timed
+    sample (the first chunks) plus `extra_chunks`, coded after the timing."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     try:
@@ -105,11 +117,20 @@ def cpu_baseline(model_path, tokens, chunk, budget_s=15.0, kv_mode=0):
     rounds = max(1, int(budget_s / per_round))
     k = min(nchunks, cores * rounds)
     t = time.perf_counter()
-    m.compress_many(tokens[:k * chunk], chunk, threads=cores)
+    first = m.compress_many(tokens[:k * chunk], chunk, threads=cores)
     dt = time.perf_counter() - t
-    return {"value": round(k * chunk / dt, 1), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"first {k} chunks x {chunk} tokens ({k * chunk} tokens) of the same workload, "
-                      f"{cores} threads, C oracle ({kind_note}), {dt:.1f} s"}
+    coded = dict(enumerate(first))
+    extra = [c for c in extra_chunks if c not in coded]
+    if extra:
+        sample = np.concatenate([tokens[c * chunk:(c + 1) * chunk] for c in extra])
+        # every extra chunk but the job's last is full, so chunk boundaries line up
+        for c, b in zip(extra, m.compress_many(sample, chunk, threads=cores)):
+            coded[c] = b
+    rec = {"value": round(k * chunk / dt, 1), "unit": "tok/s", "cores": cores, "kind": "port",
+           "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+           "sample": f"first {k} chunks x {chunk} tokens ({k * chunk} tokens) of the same workload, "
+                     f"{cores} threads, C oracle ({kind_note}), {dt:.1f} s"}
+    return rec, coded
 
 
 def main():
@@ -124,8 +145,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=0, help="truncate the workload (profiling runs only)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); chunks shard across GPUs with no "
-              f"communication, see DESIGN.md", file=sys.stderr)
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); chunks would shard across GPUs "
+              f"by chunk range with no communication during the compute", file=sys.stderr)
         sys.exit(2)
     import czip_amd
     if not os.path.exists(czip_amd.LIB_PATH):
@@ -154,21 +175,34 @@ def main():
     n = int(tokens.size)
     log(f"workload {args.workload}: {n} tokens, chunk {chunk}")
     model = czip_amd.Model(weights, device=0)
-    job = model.compress_plan(tokens, chunk)
+    t_plan = time.perf_counter()
+    job = model.compress_plan(tokens, chunk)  # device buffers + host-to-device copy of the tokens
+    plan_ms = (time.perf_counter() - t_plan) * 1000.0
     for _ in range(args.warmup):
         job.run()
-    model.reset_stats()
-    model.set_profiling(True)
+    # the rate: K steps with no per-kernel instrumentation
     t0 = time.perf_counter()
     for _ in range(args.steps):
         job.run()
     t1 = time.perf_counter()
-    model.set_profiling(False)
     ms = (t1 - t0) * 1000.0 / args.steps
-    chunks = job.fetch()
-    job.free()
-    coded = sum(len(c) for c in chunks)
     value = n / (ms / 1000.0)
+    # the per-kernel breakdown: one more step with HIP events around every launch
+    model.reset_stats()
+    model.set_profiling(True)
+    job.run()
+    model.set_profiling(False)
+    t_fetch = time.perf_counter()
+    data, offs = job.fetch_packed()
+    fetch_ms = (time.perf_counter() - t_fetch) * 1000.0
+    job.free()
+    raw = data.tobytes()
+    chunks = [raw[offs[c]:offs[c + 1]] for c in range(len(offs) - 1)]
+    coded = int(offs[-1])
+    e2e = {"value": round(n / ((plan_ms + ms + fetch_ms) / 1000.0), 1), "unit": "tok/s",
+           "plan_ms": round(plan_ms, 2), "run_ms": round(ms, 2), "fetch_ms": round(fetch_ms, 2),
+           "span": "device buffers + token upload, one step, coded bytes back to the host (packed)"}
+    prof_steps = 1
 
     # per-kernel breakdown from HIP events on the context stream
     ops = gemm_ops_per_token(cfg, kv_mode)
@@ -178,31 +212,31 @@ def main():
                  "gemm_down", "gemm_down_norm", "gemm_head", "cdf", "head_cdf", "encode"]:
         launches, tot = model.kernel_stats(name)
         if launches:
-            kernels[name] = {"launches": launches, "avg_ms": tot / launches, "ms_per_step": tot / args.steps}
+            kernels[name] = {"launches": launches, "avg_ms": tot / launches, "ms_per_step": tot / prof_steps}
     dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
     gemm_ms = sum(kernels[k]["ms_per_step"] for k in kernels if k in ops)
     gemm_tops = sum(ops[k] for k in kernels if k in ops) * nrows / (gemm_ms / 1000.0) / 1e12 if gemm_ms else 0.0
     if dom.startswith("gemm"):
-        per_launch = ops[dom] * nrows / (kernels[dom]["launches"] / args.steps)
+        per_launch = ops[dom] * nrows / (kernels[dom]["launches"] / prof_steps)
         ach = per_launch / (kernels[dom]["avg_ms"] / 1000.0) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                 "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": None, "kernel": dom}
     elif dom == "attention":
         H, T = cfg["n_heads"], chunk
         flops_per_chunk = sum(2 * 2 * H * 64 * (p + 1) for p in range(T)) * cfg["n_layers"]
-        per_launch = flops_per_chunk * (nrows // T) / (kernels[dom]["launches"] / args.steps)
+        per_launch = flops_per_chunk * (nrows // T) / (kernels[dom]["launches"] / prof_steps)
         ach = per_launch / (kernels[dom]["avg_ms"] / 1000.0) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                 "frac": round(ach / PEAK_INT8_TOPS, 5), "traffic": None, "kernel": dom}
     else:
         V = cfg["vocab_size"]
-        per_launch = (4 * V + 8) * nrows / (kernels[dom]["launches"] / args.steps)
+        per_launch = (4 * V + 8) * nrows / (kernels[dom]["launches"] / prof_steps)
         ach = per_launch / (kernels[dom]["avg_ms"] / 1000.0) / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "kernel": dom}
 
     if args.workload in TRAFFIC_WORKLOADS and roof["kernel"] in TRAFFIC_B_PER_TOKEN:
-        per_launch_tokens = n / (kernels[dom]["launches"] / args.steps)
+        per_launch_tokens = n / (kernels[dom]["launches"] / prof_steps)
         roof["traffic"] = round(TRAFFIC_B_PER_TOKEN[roof["kernel"]] * per_launch_tokens)
         roof["traffic_source"] = "rocprofv3 FETCH_SIZE/WRITE_SIZE per token x tokens per launch"
 
@@ -251,9 +285,17 @@ def main():
                                "algorithmic_bytes": alg}
 
     cpu = None
+    parity = None
     if not args.no_cpu:
         log("cpu baseline ...")
-        cpu = cpu_baseline(model_path, tokens, chunk, args.cpu_budget, kv_mode)
+        nch = len(chunks)
+        # a strided sample over the whole job, the last (ragged) chunk and the
+        # last sub-batch included, checked against the oracle besides the timed prefix
+        extra = sorted(set(np.linspace(0, nch - 1, 24).astype(int).tolist()) | {nch - 1})
+        cpu, ref = cpu_baseline(model_path, tokens, chunk, args.cpu_budget, kv_mode, extra)
+        bad = [c for c, b in ref.items() if chunks[c] != b]
+        parity = {"chunks": len(ref), "mismatches": len(bad), "first_mismatch": bad[0] if bad else None,
+                  "against": "oracle bytes of the timed CPU sample + 24 chunks strided over the job"}
     line = {
         "metric": ("compress tok/s (bit-exact .czip payload) at L4 ctx512, 1 GPU" if args.workload == DEFAULT
                    else f"compress tok/s (bit-exact .czip payload), {args.workload}, 1 GPU"),
@@ -265,15 +307,20 @@ def main():
                    "chunks": len(chunks), "kv_mode": kv_name, "parallelism": "chunks"},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "parity_sample": parity,
+        "e2e": e2e,
         "decompress": dec,
         "gemm_int8_tops": round(gemm_tops, 2),
         "coded_bytes": coded,
         "kernels": {k: {"avg_ms": round(v["avg_ms"], 4), "ms_per_step": round(v["ms_per_step"], 3),
-                        "launches_per_step": v["launches"] // args.steps} for k, v in kernels.items()},
+                        "launches_per_step": v["launches"] // prof_steps} for k, v in kernels.items()},
     }
     if cpu:
         line["speedup_vs_cpu"] = round(value / cpu["value"], 1)
     print(json.dumps(line), flush=True)
+    if parity and parity["mismatches"]:
+        log(f"parity sample: {parity['mismatches']} of {parity['chunks']} chunks differ from the oracle")
+        sys.exit(1)
 
 
 if __name__ == "__main__":

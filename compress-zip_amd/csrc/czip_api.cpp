@@ -771,6 +771,38 @@ extern "C" czip_status czip_compress_fetch(czip_job* j, uint8_t* out, int64_t sl
     return CZIP_OK;
 }
 
+extern "C" czip_status czip_compress_fetch_packed(czip_job* j, uint8_t* out, int64_t cap, int64_t* offs) {
+    if (!j || j->kind != 0 || !offs) return CZIP_E_ARG;
+    czip_ctx* c = j->ctx;
+    offs[0] = 0;
+    if (j->nchunks == 0) return CZIP_OK;
+    const size_t n = (size_t)j->nchunks;
+    std::vector<int32_t> lens(n);
+    HIPCHECK(c, hipSetDevice(c->device));
+    HIPCHECK(c, hipMemcpy(lens.data(), j->out_lens, n * 4, hipMemcpyDeviceToHost));
+    for (size_t i = 0; i < n; i++) offs[i + 1] = offs[i] + lens[i];
+    if (!out) return CZIP_OK;
+    if (offs[n] > cap) return fail(c, CZIP_E_OVERFLOW, "output smaller than the coded bytes");
+    std::vector<void*> tmp;
+    int64_t* d_offs = nullptr;
+    uint8_t* d_packed = nullptr;
+    czip_status rc;
+    if ((rc = dalloc(c, tmp, &d_offs, n)) || (rc = dalloc(c, tmp, &d_packed, (size_t)std::max<int64_t>(offs[n], 1)))) {
+        for (void* p : tmp) hipFree(p);
+        return rc;
+    }
+    hipError_t e = hipMemcpyAsync(d_offs, offs, n * 8, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        launch_pack_chunks(j->out, j->slot, j->out_lens, d_offs, (int)n, d_packed, c->stream);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(out, d_packed, (size_t)offs[n], hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    for (void* p : tmp) hipFree(p);
+    if (e != hipSuccess) return fail(c, CZIP_E_HIP, hipGetErrorString(e));
+    return CZIP_OK;
+}
+
 // ===========================================================================
 // Decompress job: streams of S chunks decode in lockstep, one token per
 // stream per step, through the same layer kernels as the prefill (M = S rows)

@@ -129,6 +129,9 @@ void launch_attention(const AttnArgs& a, int B, hipStream_t s);
 void launch_cdf(const int32_t* logits, int M, int V, const uint32_t* targets, const int32_t* lens, int T,
                 const uint16_t* lut, unsigned coef, unsigned total, int mode, uint32_t* out, int64_t out_row0,
                 hipStream_t s);
+// chunk c's lens[c] bytes from src + c * slot to dst + offs[c]
+void launch_pack_chunks(const uint8_t* src, int64_t slot, const int32_t* lens, const int64_t* offs, int n,
+                        uint8_t* dst, hipStream_t s);
 void launch_encode(const uint32_t* lohi, const int32_t* lens, int nb, int T, unsigned total, uint8_t* out,
                    int64_t slot, int32_t* out_lens, int32_t* err, hipStream_t s);
 

@@ -569,6 +569,28 @@ void launch_cdf(const int32_t* logits, int M, int V, const uint32_t* targets, co
 }
 
 // ---------------------------------------------------------------------------
+// Coded chunks from their fixed-size slots to one back-to-back buffer (the
+// chunk data layout of the container, file_format.rs:324-331), so that only
+// the coded bytes cross PCIe.  One workgroup per chunk; lens[c] <= slot.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_pack_chunks(const uint8_t* __restrict__ src, long long slot,
+                                                     const int32_t* __restrict__ lens,
+                                                     const long long* __restrict__ offs, uint8_t* __restrict__ dst) {
+    const int c = blockIdx.x;
+    const uint8_t* s = src + (size_t)c * slot;
+    uint8_t* d = dst + offs[c];
+    const int n = lens[c];
+    for (int i = threadIdx.x; i < n; i += 256) d[i] = s[i];
+}
+
+void launch_pack_chunks(const uint8_t* src, int64_t slot, const int32_t* lens, const int64_t* offs, int n,
+                        uint8_t* dst, hipStream_t s) {
+    if (n > 0)
+        hipLaunchKernelGGL(k_pack_chunks, dim3((unsigned)n), dim3(256), 0, s, src, (long long)slot, lens,
+                           (const long long*)offs, dst);
+}
+
+// ---------------------------------------------------------------------------
 // Arithmetic encoder (arith_coder.rs:26-136), one thread per chunk.
 // ---------------------------------------------------------------------------
 struct BitOut {

@@ -89,6 +89,7 @@ SIGNATURES = {
     "czip_job_run": (C.c_int32, [_P]),
     "czip_job_chunks": (C.c_int64, [_P]),
     "czip_compress_fetch": (C.c_int32, [_P, _P, C.c_int64, _P]),
+    "czip_compress_fetch_packed": (C.c_int32, [_P, _P, C.c_int64, _P]),
     "czip_job_free": (None, [_P]),
     "czip_chunk_slot_bytes": (C.c_int64, [C.c_int32]),
     "czip_decompress_plan": (C.c_int32, [_P, _P, _P, _P, _P, C.c_int32, C.POINTER(C.c_void_p)]),
@@ -354,12 +355,27 @@ class Job:
     def run(self):
         self.model._check(lib().czip_job_run(self.h))
 
-    def fetch(self):
+    def fetch_slots(self):
+        """Per-chunk coded bytes through the fixed-slot copy (czip_compress_fetch)."""
         slot = int(lib().czip_chunk_slot_bytes(self.chunk))
         buf = np.zeros(max(self.nchunks, 1) * slot, np.uint8)
         lens = np.zeros(max(self.nchunks, 1), np.int32)
         self.model._check(lib().czip_compress_fetch(self.h, _p(buf), slot, _p(lens)))
         return [bytes(buf[c * slot:c * slot + lens[c]]) for c in range(self.nchunks)]
+
+    def fetch_packed(self):
+        """(coded bytes of every chunk back to back, offsets [nchunks + 1])."""
+        offs = np.zeros(self.nchunks + 1, np.int64)
+        self.model._check(lib().czip_compress_fetch_packed(self.h, None, 0, _p(offs)))
+        buf = np.zeros(max(int(offs[-1]), 1), np.uint8)
+        self.model._check(lib().czip_compress_fetch_packed(self.h, _p(buf), buf.size, _p(offs)))
+        return buf[:int(offs[-1])], offs
+
+    def fetch(self):
+        """Per-chunk coded bytes (the chunk_results of main.rs:206-238)."""
+        buf, offs = self.fetch_packed()
+        data = buf.tobytes()
+        return [data[offs[c]:offs[c + 1]] for c in range(self.nchunks)]
 
     def free(self):
         if self.h:

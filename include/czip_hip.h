@@ -128,6 +128,13 @@ czip_status czip_job_run(czip_job* job);          /* device work only, synchrono
 int64_t     czip_job_chunks(const czip_job* job);
 /* Coded bytes of every chunk into out[c*slot ..], lengths into lens[c]. */
 czip_status czip_compress_fetch(czip_job* job, uint8_t* out, int64_t slot, int32_t* lens);
+/* The coded bytes of every chunk back to back, chunk c at out[offs[c] ..
+ * offs[c+1]) (nchunks + 1 offsets): the chunk data of the container, as
+ * czip_container_pack takes it.  Only the coded bytes leave the device.
+ * out == NULL fills offs only (offs[nchunks] = the bytes needed); a cap
+ * below that gives CZIP_E_OVERFLOW.  (The same bytes as czip_compress_fetch,
+ * which keeps the reference's one-Vec-per-chunk shape, main.rs:206-238.) */
+czip_status czip_compress_fetch_packed(czip_job* job, uint8_t* out, int64_t cap, int64_t* offs);
 void        czip_job_free(czip_job* job);
 /* Upper bound of one chunk's coded size for `chunk` tokens. */
 int64_t     czip_chunk_slot_bytes(int32_t chunk);

@@ -145,3 +145,29 @@ def test_vacc_wrap_model_wraps(orc, tmp_path):
     assert orc.vacc_wraps() == 0
     om.trace(inp, with_cum=False)
     assert orc.vacc_wraps() > 0
+
+
+@pytest.mark.parametrize("name", ["d512l8_ctx512", "d768l12_ctx4096"])
+def test_oracle_fixtures_still_match(orc, tmp_path, name):
+    """The oracle-coded fixtures of the large configurations: the seeded model
+    and ids are the ones the generators write, and (d512 / 8 layers) the
+    first and the ragged last chunk re-code to the committed bytes."""
+    import sys
+    sys.path.insert(0, GOLDEN)
+    import make_oracle_fixtures as MOF
+    from czip_amd import synth
+    fx = np.load(os.path.join(GOLDEN, name + ".npz"))
+    spec = json.loads(bytes(fx["spec"]).decode())
+    assert spec == json.loads(json.dumps(MOF.FIXTURES[name], sort_keys=True))
+    path = MOF.build_model(spec, str(tmp_path))
+    assert hashlib.sha256(open(path, "rb").read()).digest() == bytes(fx["model_sha256"])
+    ids = MOF.fixture_ids(spec, synth.MODEL_SHAPES[spec["model"]["shape"]]["vocab"])
+    assert hashlib.sha256(ids.tobytes()).digest() == bytes(fx["ids_sha256"])
+    exp = chunks_of(fx["data"], fx["offs"])
+    T = spec["chunk"]
+    assert len(exp) == (ids.size + T - 1) // T
+    if name == "d512l8_ctx512":
+        om = orc.Model.from_file(path, spec["kv_mode"])
+        last = len(exp) - 1
+        got = om.compress_many(np.concatenate([ids[:T], ids[last * T:]]), T, threads=2)
+        assert got == [exp[0], exp[last]]

@@ -88,7 +88,13 @@ def test_compress_bytes_shipped(gpu_shipped, shipped, chunk):
     n = chunk * 2 + chunk // 3
     toks = rng.integers(0, 1024, n).astype(np.uint32)
     _say(f"compress shipped chunk={chunk} n={n}")
-    got = gpu_shipped.compress_chunks(toks, chunk)
+    job = gpu_shipped.compress_plan(toks, chunk)
+    try:
+        job.run()
+        got = job.fetch()  # packed on the device
+        assert job.fetch_slots() == got  # the fixed-slot copy
+    finally:
+        job.free()
     ref = shipped.compress_many(toks, chunk, threads=8)
     assert len(got) == len(ref)
     for c, (g, r) in enumerate(zip(got, ref)):
