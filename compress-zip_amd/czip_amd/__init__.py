@@ -315,8 +315,10 @@ class Model:
         """forward + cumfreqs of every stream at its position (-1: inactive);
         with `values` (the decoders' targets) returns [S, 3] (sym, cum_lo,
         cum_hi), else the [S, V] cumulative tables."""
-        S = self._dec_S
-        tok_in = np.ascontiguousarray(tok_in, dtype=np.uint32).reshape(S)
+        tok_in = np.ascontiguousarray(tok_in, dtype=np.uint32).reshape(-1)
+        S = tok_in.size
+        if getattr(self, "_dec_S", None) not in (None, S):
+            raise ValueError(f"the decode session has {self._dec_S} streams, got {S}")
         pos = np.ascontiguousarray(pos, dtype=np.int32).reshape(S)
         if values is None:
             out = np.zeros((S, self.vocab), np.uint32)
@@ -330,6 +332,7 @@ class Model:
 
     def decode_end(self):
         lib().czip_decode_end(self._ctx)
+        self._dec_S = None
 
     # --- instrumentation ---
     def set_profiling(self, on: bool):
