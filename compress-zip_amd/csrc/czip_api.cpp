@@ -9,6 +9,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -91,6 +92,8 @@ struct czip_ctx {
     std::vector<Pending> pending;
     std::vector<hipEvent_t> event_pool;
     czip_job* dec = nullptr;  // step-wise decode session (czip_decode_begin)
+    uint8_t* noalloc = nullptr;  // this device's copy of `scratch` (czip_prefill_cdf_noalloc)
+    std::string noalloc_err;
 };
 
 struct czip_job {
@@ -288,6 +291,38 @@ extern "C" int czip_device_count(void) {
 
 extern "C" const char* czip_last_error(const czip_ctx* c) { return c ? c->err.c_str() : "null context"; }
 
+// ---------------------------------------------------------------------------
+// The one fixed device buffer of czip_prefill_cdf_noalloc: a file-scope
+// device array that the code object loader places on every GPU the library
+// runs on, held until the process ends.  In host code `scratch` names a
+// host-side stand-in, never the device memory: its device address is looked
+// up once per device (hipGetSymbolAddress, with that device current) and only
+// that address is handed to kernels.
+// ---------------------------------------------------------------------------
+constexpr size_t NOALLOC_SCRATCH_BYTES = CZIP_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+std::map<int, uint8_t*> g_scratch_addr;  // device -> address of that device's `scratch`
+
+// device must be current
+hipError_t scratch_address(int device, uint8_t** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    auto it = g_scratch_addr.find(device);
+    if (it != g_scratch_addr.end()) {
+        *out = it->second;
+        return hipSuccess;
+    }
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) return e != hipSuccess ? e : hipErrorInvalidSymbol;
+    g_scratch_addr[device] = (uint8_t*)p;
+    *out = (uint8_t*)p;
+    return hipSuccess;
+}
+}  // namespace
+
 extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ctx** out) {
     if (!w || !out) return CZIP_E_ARG;
     *out = nullptr;
@@ -365,6 +400,15 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
         launch_gemm(g, EPI_REQ, c->stream);
         HIPCHECK(C, hipGetLastError());
         HIPCHECK(C, hipStreamSynchronize(c->stream));
+    }
+    {
+        // the no-alloc entry point's buffer on this device (its failure only
+        // disables that entry point)
+        hipError_t e = scratch_address(device, &c->noalloc);
+        if (e != hipSuccess) {
+            c->noalloc = nullptr;
+            c->noalloc_err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+        }
     }
     *out = c.release();
     return CZIP_OK;
@@ -1096,4 +1140,92 @@ extern "C" void czip_decode_end(czip_ctx* c) {
     hipSetDevice(c->device);
     hipStreamSynchronize(c->stream);
     free_decode_session(c);
+}
+
+// ===========================================================================
+// czip_prefill_cdf without allocation: the same intervals, with every
+// intermediate in the device's fixed `scratch` buffer
+// ===========================================================================
+namespace {
+
+// Bump allocator over a fixed buffer (base == nullptr: size only).
+struct Carve {
+    uint8_t* base;
+    size_t off = 0;
+    template <typename T>
+    T* take(size_t count) {
+        T* p = base ? (T*)(base + off) : nullptr;
+        off += (std::max<size_t>(count * sizeof(T), 1) + 255) & ~(size_t)255;
+        return p;
+    }
+};
+
+// the forward's buffers for B chunks of T rows (alloc_scratch's set, less
+// what the fused kernels never touch) plus the row prep's
+int32_t* carve_prefill(czip_ctx* c, czip_job* j, Carve& cv, int B, int T) {
+    const size_t M = (size_t)B * T, d = (size_t)c->cfg.d_model, F = (size_t)c->cfg.d_ff, V = (size_t)c->cfg.vocab;
+    int32_t* err = cv.take<int32_t>(1);
+    j->inp = cv.take<uint32_t>(M);
+    j->tgt = cv.take<uint32_t>(M);
+    j->lens = cv.take<int32_t>((size_t)B);
+    j->x = cv.take<int16_t>(M * d);
+    j->xn = cv.take<int8_t>(M * d);
+    j->q8 = cv.take<int8_t>(M * d);
+    j->attn = cv.take<int8_t>(M * d);
+    j->y8 = c->rn_fused ? nullptr : cv.take<int8_t>(M * d);
+    j->r8 = cv.take<int8_t>(M * F);
+    j->kc = cv.take<int8_t>(M * (size_t)c->KH * 64);
+    j->vc = cv.take<int8_t>((size_t)B * pad64(T) * (size_t)c->KH * 64);
+    j->logits = c->head_fused ? nullptr : cv.take<int32_t>(M * V);
+    return err;
+}
+
+}  // namespace
+
+extern "C" czip_status czip_prefill_cdf_noalloc(czip_ctx* c, const uint32_t* d_targets, const int32_t* d_lens,
+                                                int32_t B, int32_t T, uint32_t* d_cum_lohi) {
+    if (!c) return CZIP_E_ARG;
+    if (!d_targets || !d_lens || !d_cum_lohi || B < 0) return fail(c, CZIP_E_ARG, "null argument");
+    if (((uintptr_t)d_targets & 3) || ((uintptr_t)d_lens & 3) || ((uintptr_t)d_cum_lohi & 7))
+        return fail(c, CZIP_E_ARG, "targets / lens must be 4-byte and cum_lohi 8-byte aligned");
+    if (B == 0) return CZIP_OK;
+    if (T < 1) return fail(c, CZIP_E_ARG, "T must be >= 1");
+    if (T > c->cfg.context_length || T > c->cfg.max_seq_len)
+        return fail(c, CZIP_E_RANGE, "chunk length exceeds the RoPE LUT / KV cache (lut.rs:169-177)");
+    if ((uint32_t)c->cfg.vocab <= BOS) return fail(c, CZIP_E_TOKEN, "BOS token 1022 is outside the vocabulary");
+    if (!c->noalloc) return fail(c, CZIP_E_HIP, "no scratch buffer on this device: " + c->noalloc_err);
+    czip_job j;
+    j.ctx = c;
+    Carve size{nullptr};
+    carve_prefill(c, &j, size, B, T);
+    if (size.off > NOALLOC_SCRATCH_BYTES)
+        return fail(c, CZIP_E_RANGE,
+                    "B * T = " + std::to_string((long long)B * T) + " rows need " + std::to_string(size.off) +
+                        " bytes of scratch; the no-alloc entry point holds " + std::to_string(NOALLOC_SCRATCH_BYTES));
+    HIPCHECK(c, hipSetDevice(c->device));
+    hipStream_t s = c->stream;
+    Carve cv{c->noalloc};
+    int32_t* err = carve_prefill(c, &j, cv, B, T);
+    const int M = B * T, V = c->cfg.vocab;
+    launch_prep_rows(d_targets, d_lens, B, T, V, j.inp, j.tgt, j.lens, d_cum_lohi, err, s);
+    czip_status rc = forward_batch(c, &j, B, T, !c->head_fused);
+    if (rc) return rc;
+    if (c->head_fused) {
+        HeadCdfArgs h{};
+        h.A = j.xn; h.W = c->head_wf; h.M = M; h.K = c->cfg.d_model; h.V = V; h.targets = j.tgt; h.lens = j.lens;
+        h.T = T; h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total;
+        h.out = d_cum_lohi; h.out_row0 = 0;
+        Timed t(c, "head_cdf");
+        launch_head_cdf(h, s);
+    } else {
+        Timed t(c, "cdf");
+        launch_cdf(j.logits, M, V, j.tgt, j.lens, T, c->lut, c->cfg.coef_q24, c->cfg.target_total, 0, d_cum_lohi, 0, s);
+    }
+    HIPCHECK(c, hipGetLastError());
+    int32_t h_err = 0;
+    HIPCHECK(c, hipMemcpyAsync(&h_err, err, 4, hipMemcpyDeviceToHost, s));
+    HIPCHECK(c, hipStreamSynchronize(s));
+    resolve_events(c);
+    if (h_err) return fail(c, CZIP_E_TOKEN, "a target id >= vocab in a live row");
+    return CZIP_OK;
 }

@@ -129,6 +129,10 @@ void launch_attention(const AttnArgs& a, int B, hipStream_t s);
 void launch_cdf(const int32_t* logits, int M, int V, const uint32_t* targets, const int32_t* lens, int T,
                 const uint16_t* lut, unsigned coef, unsigned total, int mode, uint32_t* out, int64_t out_row0,
                 hipStream_t s);
+// [B, T] coder targets -> prefill inputs / targets, clamped lens, zeroed
+// intervals, and *err = 1 if a live target is >= V (err cleared first)
+void launch_prep_rows(const uint32_t* targets, const int32_t* lens_in, int B, int T, int V, uint32_t* inp,
+                      uint32_t* tgt, int32_t* lens, uint32_t* out, int32_t* err, hipStream_t s);
 // chunk c's lens[c] bytes from src + c * slot to dst + offs[c]
 void launch_pack_chunks(const uint8_t* src, int64_t slot, const int32_t* lens, const int64_t* offs, int n,
                         uint8_t* dst, hipStream_t s);

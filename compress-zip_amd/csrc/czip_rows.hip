@@ -569,6 +569,49 @@ void launch_cdf(const int32_t* logits, int M, int V, const uint32_t* targets, co
 }
 
 // ---------------------------------------------------------------------------
+// Rows of a [B, T] block of coder targets for the prefill (main.rs:220-226):
+// the input of row (b, p) is BOS at p = 0, else target (b, p - 1); lens are
+// clamped to [0, T]; rows past a chunk's length get zeros, and so does their
+// (cum_lo, cum_hi) in out (the head writes only live rows).  A live target
+// >= V sets *err and reads as 0.  One thread per row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_prep_rows(const uint32_t* __restrict__ targets,
+                                                   const int32_t* __restrict__ lens_in, int B, int T, unsigned V,
+                                                   uint32_t* __restrict__ inp, uint32_t* __restrict__ tgt,
+                                                   int32_t* __restrict__ lens, uint32_t* __restrict__ out,
+                                                   int32_t* __restrict__ err) {
+    const long long r = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (r >= (long long)B * T) return;
+    const int b = (int)(r / T), p = (int)(r - (long long)b * T);
+    const int n = min(max(lens_in[b], 0), T);
+    if (p == 0) lens[b] = n;
+    uint32_t t = 0, prev = 0;
+    if (p < n) {
+        t = targets[r];
+        if (t >= V) {
+            atomicOr(err, 1);
+            t = 0;
+        }
+        prev = p == 0 ? BOS_TOKEN : targets[r - 1];
+        prev = prev < V ? prev : 0u;
+    }
+    inp[r] = prev;
+    tgt[r] = t;
+    *(uint2*)(out + 2 * r) = make_uint2(0u, 0u);
+}
+
+__global__ void k_zero_i32(int32_t* p) { *p = 0; }
+
+void launch_prep_rows(const uint32_t* targets, const int32_t* lens_in, int B, int T, int V, uint32_t* inp,
+                      uint32_t* tgt, int32_t* lens, uint32_t* out, int32_t* err, hipStream_t s) {
+    const long long M = (long long)B * T;
+    hipLaunchKernelGGL(k_zero_i32, dim3(1), dim3(1), 0, s, err);
+    if (M > 0)
+        hipLaunchKernelGGL(k_prep_rows, dim3((unsigned)((M + 255) / 256)), dim3(256), 0, s, targets, lens_in, B, T,
+                           (unsigned)V, inp, tgt, lens, out, err);
+}
+
+// ---------------------------------------------------------------------------
 // Coded chunks from their fixed-size slots to one back-to-back buffer (the
 // chunk data layout of the container, file_format.rs:324-331), so that only
 // the coded bytes cross PCIe.  One workgroup per chunk; lens[c] <= slot.

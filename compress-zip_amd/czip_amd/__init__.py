@@ -85,6 +85,7 @@ SIGNATURES = {
     "czip_forward_logits": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
     "czip_prefill_cdf": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
     "czip_prefill_cumfreqs": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
+    "czip_prefill_cdf_noalloc": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
     "czip_compress_plan": (C.c_int32, [_P, _P, C.c_int64, C.c_int32, C.POINTER(C.c_void_p)]),
     "czip_job_run": (C.c_int32, [_P]),
     "czip_job_chunks": (C.c_int64, [_P]),

@@ -114,6 +114,25 @@ czip_status czip_forward_logits(czip_ctx* ctx, const uint32_t* inputs, const int
 czip_status czip_prefill_cdf(czip_ctx* ctx, const uint32_t* targets, const int32_t* lens,
                              int32_t B, int32_t T, uint32_t* cum_lohi);
 
+/* ---- czip_prefill_cdf without allocation.  No counterpart in the
+ *      reference: this is for callers that cannot allocate device memory
+ *      (code under HIP graph capture, tight serving loops, harnesses that
+ *      forbid hipMalloc).  The same (cum_lo, cum_hi) as czip_prefill_cdf, but
+ *      targets [B*T], lens [B] and cum_lohi [B*T, 2] are DEVICE pointers on
+ *      the context's device (4-, 4- and 8-byte aligned, as hipMalloc
+ *      memory is), and every intermediate lives in one fixed
+ *      device buffer of CZIP_NOALLOC_SCRATCH_BYTES per GPU (held from the
+ *      library's load until the process ends): no hipMalloc / hipFree.
+ *      B * T rows that need more than that give CZIP_E_RANGE (the shipped
+ *      model needs ~3.5 KB per row: about 19K rows, e.g. 37 chunks of 512).
+ *      lens are clamped to [0, T]; rows past a chunk's length come back 0; a
+ *      target >= vocab in a live row gives CZIP_E_TOKEN.  Synchronous.  All
+ *      calls on one GPU share its buffer, so calls that overlap in time on
+ *      one GPU (several contexts or host threads) race. ---- */
+#define CZIP_NOALLOC_SCRATCH_BYTES (64ull << 20)
+czip_status czip_prefill_cdf_noalloc(czip_ctx* ctx, const uint32_t* d_targets, const int32_t* d_lens,
+                                     int32_t B, int32_t T, uint32_t* d_cum_lohi);
+
 /* Full cumulative tables (debug / parity), host [B*T, V]. */
 czip_status czip_prefill_cumfreqs(czip_ctx* ctx, const uint32_t* inputs, const int32_t* lens,
                                   int32_t B, int32_t T, uint32_t* cumfreqs);
