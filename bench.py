@@ -30,6 +30,12 @@ PEAK_HBM_GBS = 8000.0       # GB/s
 TRAFFIC_B_PER_TOKEN = {"attention": 523 + 405, "qkv_table": 13 + 512, "gemm_o_norm": 397 + 1152,
                        "gemm_down_norm": 1814 + 384, "gemm_up": 556 + 1024, "head_cdf": 391 + 8}
 TRAFFIC_WORKLOADS = ("v001_L4_ctx512_text64MiB",)
+# Prefill attention: wave64 VALU instructions (MFMA excluded) per 16-row x 64-key tile,
+# from SQ_INSTS_VALU - SQ_INSTS_VALU_MFMA_I8 on the same workload
+# (profiles/counters_compress_v001_ctx512_text8Mtok.md); the VALU issue peak is one wave64
+# instruction per 4 cycles per SIMD: 1024 SIMDs x 2.4 GHz / 4.
+ATTN_VALU_PER_TILE = {"v001_L4_ctx512_text64MiB": 1305}
+PEAK_VALU_GINST = 1024 * 2.4 / 4 * 1e9 / 1e9
 
 WORKLOADS = {
     # shipped model, level 4 (512-token chunks), 64 MiB of seeded synthetic text
@@ -228,6 +234,15 @@ def main():
         ach = per_launch / (kernels[dom]["avg_ms"] / 1000.0) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                 "frac": round(ach / PEAK_INT8_TOPS, 5), "traffic": None, "kernel": dom}
+        if args.workload in ATTN_VALU_PER_TILE and not args.tokens:
+            # the bound it actually hits: VALU issue (16-row x 64-key tiles, causal)
+            nq16 = (T + 15) // 16
+            tiles_chunk = H * sum((16 * b + 15) // 64 + 1 for b in range(nq16))
+            tiles_launch = tiles_chunk * (nrows // T) / (kernels[dom]["launches"] / prof_steps)
+            gi = ATTN_VALU_PER_TILE[args.workload] * tiles_launch / (kernels[dom]["avg_ms"] / 1000.0) / 1e9
+            roof["valu"] = {"per_tile": ATTN_VALU_PER_TILE[args.workload], "tiles_per_launch": round(tiles_launch),
+                            "achieved": round(gi, 1), "peak": PEAK_VALU_GINST, "unit": "G wave64 VALU inst/s",
+                            "frac": round(gi / PEAK_VALU_GINST, 4)}
     else:
         V = cfg["vocab_size"]
         per_launch = (4 * V + 8) * nrows / (kernels[dom]["launches"] / prof_steps)
