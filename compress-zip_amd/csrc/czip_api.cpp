@@ -340,7 +340,7 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
     const size_t d = (size_t)w->d_model, F = (size_t)w->d_ff, V = (size_t)w->vocab, G = (size_t)w->n_kv_heads;
     c->KH = w->kv_mode == CZIP_KV_GQA ? w->n_kv_heads : 1;
     c->rn_fused = gemm_rn_supported(w->d_model) && getenv("CZIP_UNFUSED_NORM") == nullptr;
-    c->head_fused = head_cdf_supported(w->vocab) && w->coef_q24 < (1u << 24) && getenv("CZIP_UNFUSED_HEAD") == nullptr;
+    c->head_fused = head_cdf_supported(w->vocab) && w->coef_q24 < (1u << 23) && getenv("CZIP_UNFUSED_HEAD") == nullptr;
     czip_ctx* C = c.get();
 #define UP(dst, src, n) if ((rc = upload(C, &dst, src, n))) return rc;
     UP(c->embed, w->embed, V * d)

@@ -13,9 +13,16 @@ namespace czip {
 // wave's range (t < CT).
 constexpr int HBM_ROWS = 64, HNW = 16;
 
+// E(t) (exp_q16 at table step t, lut.rs:213-235) for every step t < 4096 and
+// t = 4096 standing for all larger ones: (65536 >> ip) * lut[t & 255] rounds
+// to at most 1 for ip = t >> 8 >= 16, and the clamp makes it 1.  Entry 4097
+// is E(0) = 65535 of a logit equal to the max (diff >= 0 in the reference,
+// whatever lut[0] holds).
+constexpr int ETAB_N = 4098;
+
 struct HeadLds {
     int8_t As[2][HBM_ROWS * 64] __attribute__((aligned(16)));
-    unsigned lut32[256];
+    unsigned etab[ETAB_N + 2];
     int red_a[HNW][HBM_ROWS];
     unsigned red_b[HNW][HBM_ROWS], red_c[HNW][HBM_ROWS];
     int row_i[HBM_ROWS], row_am[HBM_ROWS];
@@ -41,7 +48,11 @@ __device__ __forceinline__ void head_freqs(const int8_t* A, int M, int K, const 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nb = wave * CT * 16;
     const int lr = lane & 15, c4 = (lane >> 4) * 4;
-    if (tid < 256) L.lut32[tid] = (unsigned)lut[tid] << 16;
+    for (int t = tid; t < ETAB_N; t += 64 * HNW) {
+        const unsigned ip = (unsigned)t >> 8;
+        const unsigned x = ip >= 16u ? 1u : ((65536u >> ip) * (unsigned)lut[t & 255] + 0x8000u) >> 16;
+        L.etab[t] = t == ETAB_N - 1 ? 65535u : (x < 1u ? 1u : (x > 65535u ? 65535u : x));
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -68,24 +79,35 @@ __device__ __forceinline__ void head_freqs(const int8_t* A, int M, int K, const 
         L.row_i[lane] = mx;
     }
     __syncthreads();
-    // 2. first argmax and S = sum of e = E(l - max)
+    // 2. first argmax and S = sum of e = E(l - max).  The table step of
+    // E(-n) is t = floor((n * coef + 2^23) / 2^24): for coef < 2^24 the high
+    // word of n * (coef * 256) + 2^31, one 32 x 32 + 64 multiply-add; every
+    // step past 4096 reads as 4096.  The lane's columns are walked from the
+    // last, so the last match left is its first maximum.
+    // With c = coef * 256 (< 2^31: coef < 2^23) and K = mx * c + 2^31 per
+    // row, n * c + 2^31 = K - l * c: one signed 32 x 32 + 64 multiply-add of
+    // the logit.  The equal-to-max case is an index (entry 4097), so every
+    // element reads the table unconditionally; the argmax is kept as the
+    // lane's element index k (an inline constant) and turned into a column once.
+    const int negc = -(int)(coef << 8);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int mx = L.row_i[i * 16 + lr];
-        int am = 0x7FFFFFFF;
+        const long long kr = (long long)mx * (long long)(coef << 8) + 0x80000000ll;
+        int ak = 64;
         unsigned s = 0;
 #pragma unroll
-        for (int t = 0; t < CT; t++)
+        for (int t = CT - 1; t >= 0; t--)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int col = nb + t * 16 + c4 + r;
+            for (int r = 3; r >= 0; r--) {
                 const int l = acc[i][t][r];
-                am = (l == mx && col < am) ? col : am;
-                const unsigned x = exp_q16_t((unsigned)mx - (unsigned)l, L.lut32, coef << 8);
-                const unsigned e = l == mx ? 65535u : x;  // E(0) is 65535 whatever lut[0]
+                ak = l == mx ? t * 4 + r : ak;
+                const unsigned st = min((unsigned)((unsigned long long)((long long)l * (long long)negc + kr) >> 32), 4096u);
+                const unsigned e = L.etab[l == mx ? ETAB_N - 1 : (int)st];
                 acc[i][t][r] = (int)e;
                 s += e;
             }
+        int am = ak == 64 ? 0x7FFFFFFF : nb + (ak >> 2) * 16 + c4 + (ak & 3);
         am = min(am, __shfl_xor(am, 16, 64));
         am = min(am, __shfl_xor(am, 32, 64));
         s += (unsigned)__shfl_xor((int)s, 16, 64);
