@@ -79,7 +79,7 @@ def gemm_ops_per_token(cfg, kv_mode):
     d, F, V, G = cfg["d_model"], cfg["d_ff"], cfg["vocab_size"], cfg["n_kv_heads"]
     qkv_n = d + 2 * G * 64 if kv_mode == 1 else d + 128
     per_layer = {"gemm_qkv": qkv_n * d, "gemm_o": d * d, "gemm_o_norm": d * d, "gemm_up": 2 * F * d,
-                 "gemm_down": d * F, "gemm_down_norm": d * F}
+                 "gemm_down": d * F, "gemm_down_norm": d * F, "ffn": 2 * F * d + d * F}
     out = {k: 2 * v * cfg["n_layers"] for k, v in per_layer.items()}
     # layer 0's QKV projection is a per-token table (qkv_table: RoPE and scatter only)
     out["gemm_qkv"] = 2 * qkv_n * d * (cfg["n_layers"] - 1)
@@ -215,7 +215,7 @@ def main():
     nrows = ((n + chunk - 1) // chunk) * chunk
     kernels = {}
     for name in ["prep", "embed_norm", "qkv_table", "gemm_qkv", "attention", "gemm_o", "gemm_o_norm", "row_norm", "gemm_up",
-                 "gemm_down", "gemm_down_norm", "gemm_head", "cdf", "head_cdf", "encode"]:
+                 "gemm_down", "gemm_down_norm", "ffn", "gemm_head", "cdf", "head_cdf", "encode"]:
         launches, tot = model.kernel_stats(name)
         if launches:
             kernels[name] = {"launches": launches, "avg_ms": tot / launches, "ms_per_step": tot / prof_steps}
@@ -281,7 +281,7 @@ def main():
         djob.free()
         dk = {}
         for name in ["dec_init", "dec_prep", "embed_norm", "qkv_table", "gemm_qkv", "attn_decode", "gemm_o", "gemm_o_norm",
-                     "row_norm", "gemm_up", "gemm_down", "gemm_down_norm", "head_dec", "gemm_head", "cdf_decode"]:
+                     "row_norm", "gemm_up", "gemm_down", "gemm_down_norm", "ffn", "head_dec", "gemm_head", "cdf_decode"]:
             launches, tot = model.kernel_stats(name)
             if launches:
                 dk[name] = {"ms": round(tot, 3), "launches": launches}

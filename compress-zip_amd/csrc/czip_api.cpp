@@ -21,11 +21,13 @@ using namespace czip;
 namespace {
 
 constexpr uint32_t BOS = 1022u;  // main.rs:222, 387
+constexpr int FFN_MIN_ROWS = 1 << 19;  // rows from which a layer's FFN runs as one fused kernel
 
 struct DevLayer {
     int8_t *attn_norm = nullptr, *post_attn_norm = nullptr, *ffn_norm = nullptr, *post_ffn_norm = nullptr;
     int8_t *qkv_w = nullptr, *out_w = nullptr, *up_w = nullptr, *down_w = nullptr, *sink = nullptr;
     int8_t *out_wf = nullptr, *down_wf = nullptr;  // fragment-major copies (row GEMM)
+    int8_t* up_wf16 = nullptr;  // fragment-major, gate and up tiles interleaved per 16 features (fused FFN)
     int32_t* score_mult = nullptr;
     int qkv_mult, out_mult, up_mult, down_mult, qkv_shift, out_shift, up_shift, down_shift;
     int qkv_n;  // QKV rows the attention reads
@@ -75,6 +77,7 @@ struct czip_ctx {
     int KH = 1;  // cached KV heads per layer
     bool rn_fused = false;  // residual + norms fused into the row GEMM (gemm_rn_supported(d_model))
     bool head_fused = false;  // LM head fused with the coder interval stage / decode step (head_cdf_supported(vocab))
+    bool ffn_fused = false;   // up + ReGLU + down + norms in one kernel (ffn_supported(d_model, d_ff))
     std::vector<void*> allocs;
     int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr, *head_wf = nullptr;
     int8_t* embed_xn = nullptr;  // rmsnorm(embed[v], layer 0's attn_norm) for every token v
@@ -341,6 +344,7 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
     c->KH = w->kv_mode == CZIP_KV_GQA ? w->n_kv_heads : 1;
     c->rn_fused = gemm_rn_supported(w->d_model) && getenv("CZIP_UNFUSED_NORM") == nullptr;
     c->head_fused = head_cdf_supported(w->vocab) && w->coef_q24 < (1u << 23) && getenv("CZIP_UNFUSED_HEAD") == nullptr;
+    c->ffn_fused = c->rn_fused && ffn_supported(w->d_model, w->d_ff) && getenv("CZIP_UNFUSED_FFN") == nullptr;
     czip_ctx* C = c.get();
 #define UP(dst, src, n) if ((rc = upload(C, &dst, src, n))) return rc;
     UP(c->embed, w->embed, V * d)
@@ -374,6 +378,14 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
         UP(D.up_w, perm.data(), 2 * F * d)
         UP(D.down_w, L.down_w, d * F)
         if ((rc = upload_frag_major(C, &D.down_wf, L.down_w, d, F))) return rc;
+        if (c->ffn_fused) {
+            // rows 32 g .. +16 = gate rows 16 g .., rows 32 g + 16 .. = the matching up rows
+            for (size_t g = 0; g < F / 16; g++) {
+                memcpy(&perm[(g * 32) * d], L.up_w + (g * 16) * d, 16 * d);
+                memcpy(&perm[(g * 32 + 16) * d], L.up_w + (F + g * 16) * d, 16 * d);
+            }
+            if ((rc = upload_frag_major(C, &D.up_wf16, perm.data(), 2 * F, d))) return rc;
+        }
         UP(D.score_mult, L.score_mult, (size_t)w->n_heads)
         if (L.sink_key) { UP(D.sink, L.sink_key, 64) }
         D.attn_general = attention_needs_general(w->exp2_lut, L.score_mult, w->n_heads);
@@ -511,6 +523,22 @@ void post_attention(czip_ctx* c, czip_job* j, int l, int M) {
         set_requant(o, L.out_mult, L.out_shift);
         { Timed t(c, "gemm_o"); launch_gemm(o, EPI_REQ, s); }
         { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.ffn_norm, L.post_attn_norm, M, d, j->xn, s); }
+    }
+    // the fused FFN walks 128-row strips with one workgroup per CU: it pays
+    // off for prefill sub-batches, while a decode step's few thousand rows
+    // balance better over the separate kernels' 64-row blocks
+    if (c->ffn_fused && M >= FFN_MIN_ROWS) {
+        GemmArgs u{}, dn{};  // requantization parameters of the two products
+        u.K = d; set_requant(u, L.up_mult, L.up_shift);
+        dn.K = F; set_requant(dn, L.down_mult, L.down_shift);
+        FfnArgs f{};
+        f.xn = j->xn; f.Wup = L.up_wf16; f.Wdf = L.down_wf; f.M = M; f.d = d; f.F = F;
+        f.up_mult = u.mult; f.up_shift = u.shift; f.up_fast = u.rq_fast; f.up_scale = u.rq_scale;
+        f.dn_mult = dn.mult; f.dn_shift = dn.shift; f.dn_fast = dn.rq_fast; f.dn_scale = dn.rq_scale;
+        f.w1 = L.post_ffn_norm; f.w2 = next; f.x_in = j->x; f.x_out = last ? nullptr : j->x; f.xn_out = j->xn;
+        Timed t(c, "ffn");
+        launch_ffn(f, s);
+        return;
     }
     GemmArgs u{};
     u.A = j->xn; u.W = L.up_w; u.M = M; u.N = 2 * F; u.K = d; u.out8 = j->r8; u.ldo = F;

@@ -192,6 +192,33 @@ __device__ __forceinline__ int inv_rms_q15_fast(int mean_sq) {
     return (int)(inv < 1u ? 1u : (inv > 32768u ? 32768u : inv));
 }
 
+// model.rs:280-300.  Fast path: |v * mult| < 2^53, so v * mult * 2^-shift is
+// exact in f64, and |v * mult * 2^-shift| < 2^31, so its rint (half to even,
+// like sra_rne_tte_s64_to_s32) is one FMA and the clamp an integer med3.
+template <bool FAST>
+__device__ __forceinline__ int rq(int v, double scale, int mult, int shift) {
+    if (FAST) return clamp127(rint_fma_i32((double)v, scale));
+    return requant(v, mult, shift);
+}
+
+__device__ __forceinline__ unsigned pack4i(int a, int b, int c, int d) {
+    return (unsigned)(a & 0xFF) | ((unsigned)(b & 0xFF) << 8) | ((unsigned)(c & 0xFF) << 16) | ((unsigned)d << 24);
+}
+
+__device__ __forceinline__ void unpack4s(unsigned w, int* o) {
+    o[0] = (int)(int8_t)(w & 0xFF);
+    o[1] = (int)(int8_t)((w >> 8) & 0xFF);
+    o[2] = (int)(int8_t)((w >> 16) & 0xFF);
+    o[3] = (int)(int8_t)(w >> 24);
+}
+
+// rmsnorm.rs:40-75 for one element: clamp(sra_rne((x * w) * inv, 15)).  |x|, |w| <= 127 and
+// 1 <= inv <= 2^15, so x * w is an exact 24-bit multiply and (x * w) * (inv * 2^-15)
+// is exact in f64 with |.| < 2^15: its rint (half to even) is one FMA.
+__device__ __forceinline__ int rms_el(int x, int w, double inv_s15) {
+    return clamp127(rint_fma_i32((double)__mul24(x, w), inv_s15));
+}
+
 // lut.rs:213-235 / softmax_cdf.rs:55-77
 __device__ __forceinline__ unsigned exp_q16(int diff, const uint16_t* lut, unsigned coef) {
     if (diff >= 0) return 65535u;

@@ -80,6 +80,27 @@ size_t gemm_rn_ws_bytes(int M, int d);
 void launch_rn_splitk_epi(const RowGemmArgs& a, const int32_t* part, int splits, hipStream_t s);
 void launch_gemm_rn(const RowGemmArgs& a, hipStream_t s);
 
+// The FFN of one layer in one kernel (model.rs:438-468 from the pre-FFN norm's
+// output): xn_out = rmsnorm(clamp(x), w2) with x = x_in + rmsnorm(requant(
+// reglu(requant(xn W_up^T)) W_down^T), w1); the ReGLU output stays on chip.
+struct FfnArgs {
+    const int8_t* xn;       // [M, d] input rows (may alias xn_out: a strip is read before it is written)
+    const int8_t* Wup;      // [2F, d] fragment-major, tile 2g = gate rows 16g.., tile 2g + 1 = the matching up rows
+    const int8_t* Wdf;      // [d, F] fragment-major
+    int M, d, F;
+    int up_mult, up_shift, up_fast;
+    double up_scale;
+    int dn_mult, dn_shift, dn_fast;
+    double dn_scale;
+    const int8_t* w1;       // post-FFN norm
+    const int8_t* w2;       // the next pre-norm (or the final norm)
+    const int16_t* x_in;    // [M, d] residual stream
+    int16_t* x_out;         // [M, d] or nullptr (after the last layer)
+    int8_t* xn_out;         // [M, d]
+};
+bool ffn_supported(int d, int F);
+void launch_ffn(const FfnArgs& a, hipStream_t s);
+
 // LM head + logits -> (cum_lo, cum_hi) of each row's target (k_cdf mode 0)
 // without the int32 logits leaving the chip; V in {512, 1024}.
 struct HeadCdfArgs {

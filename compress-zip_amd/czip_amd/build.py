@@ -16,7 +16,8 @@ CSRC = os.path.join(ROOT, "csrc")
 BUILD_DIR = os.path.join(ROOT, "_build")
 LIB_PATH = os.path.join(ROOT, "libczip_hip.so")
 
-SOURCES = ["czip_rows.hip", "czip_gemm.hip", "czip_head.hip", "czip_attention.hip", "czip_decode.hip", "czip_api.cpp",
+SOURCES = ["czip_rows.hip", "czip_gemm.hip", "czip_head.hip", "czip_attention.hip", "czip_decode.hip", "czip_ffn.hip",
+           "czip_api.cpp",
            "czm_loader.cpp", "czip_tokenizer.cpp", "czip_container.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",

@@ -198,6 +198,21 @@ def test_unfused_norm_path(amd, orc, tmp_path, monkeypatch):
         assert np.array_equal(out, toks)
 
 
+def test_unfused_ffn_path(gpu_shipped, shipped, monkeypatch, amd):
+    """The separate FFN up + ReGLU and down + norm kernels behind the fused
+    FFN kernel (switched off by environment at context creation)."""
+    from czip_amd import synth
+    monkeypatch.setenv("CZIP_UNFUSED_FFN", "1")
+    gm = amd.Model(amd.ModelWeights(MODEL_PATH))
+    lens = [512, 300]
+    toks = synth.zipf_ids(sum(lens), 1024, seed=93)
+    _say("compress shipped, FFN unfused")
+    ref = shipped.compress_many(toks, 512, threads=2)
+    assert gm.compress_chunks(toks, 512) == ref
+    assert gpu_shipped.compress_chunks(toks, 512) == ref
+    assert np.array_equal(gm.decompress_chunks(ref, lens), toks)
+
+
 def test_requant_general_path(amd, orc, tmp_path):
     """Requantization outside the GEMMs' f64 fast path (|mult| >= 2^26, negative
     multipliers, shift <= 0) against the oracle."""
