@@ -83,6 +83,7 @@ struct czip_ctx {
     int8_t* embed_xn = nullptr;  // rmsnorm(embed[v], layer 0's attn_norm) for every token v
     int8_t* qkv_tab = nullptr;   // layer 0's requantized QKV projection of embed_xn[v] (before RoPE)
     uint16_t* lut = nullptr;
+    uint16_t* etab = nullptr;    // attention's exp table by step, weights as offset bytes (attn_etab_host)
     int16_t *rcos = nullptr, *rsin = nullptr;
     std::vector<DevLayer> layers;
     std::string err;
@@ -352,6 +353,11 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
     UP(c->head_w, w->head_w, V * d)
     if ((rc = upload_frag_major(C, &c->head_wf, w->head_w, V, d))) return rc;
     UP(c->lut, w->exp2_lut, 256)
+    {
+        std::vector<uint16_t> et(ETB_PAD);
+        attn_etab_host(w->exp2_lut, et.data());
+        UP(c->etab, et.data(), et.size())
+    }
     UP(c->rcos, w->rope_cos, (size_t)w->rope_len)
     UP(c->rsin, w->rope_sin, (size_t)w->rope_len)
     c->layers.resize((size_t)w->n_layers);
@@ -607,7 +613,7 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T, bool head = t
         }
         AttnArgs a{};
         a.q = j->q8; a.kc = j->kc; a.vc = j->vc; a.TP = pad64(T); a.lens = j->lens; a.score_mult = L.score_mult;
-        a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = M; a.T = T; a.H = H; a.G = c->cfg.n_kv_heads;
+        a.sink = L.sink; a.lut = c->lut; a.etab = c->etab; a.out = j->attn; a.M = M; a.T = T; a.H = H; a.G = c->cfg.n_kv_heads;
         a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
         a.general = L.attn_general;
         { Timed t(c, "attention"); launch_attention(a, nb, s); }
@@ -986,7 +992,7 @@ static czip_status run_decompress(czip_job* j) {
                 }
                 AttnArgs a{};
                 a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = j->d_ntok + g0; a.score_mult = L.score_mult;
-                a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = S; a.T = TP; a.H = H; a.G = c->cfg.n_kv_heads;
+                a.sink = L.sink; a.lut = c->lut; a.etab = c->etab; a.out = j->attn; a.M = S; a.T = TP; a.H = H; a.G = c->cfg.n_kv_heads;
                 a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;
                 a.general = L.attn_general;
                 { Timed t(c, "attn_decode"); launch_attn_decode(a, S, p, s); }
@@ -1140,7 +1146,7 @@ extern "C" czip_status czip_decode_step(czip_ctx* c, const uint32_t* tok_in, con
         }
         AttnArgs a{};
         a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = j->d_ntok; a.score_mult = L.score_mult;
-        a.sink = L.sink; a.lut = c->lut; a.out = j->attn; a.M = S; a.T = TP; a.H = c->cfg.n_heads; a.G = c->cfg.n_kv_heads;
+        a.sink = L.sink; a.lut = c->lut; a.etab = c->etab; a.out = j->attn; a.M = S; a.T = TP; a.H = c->cfg.n_heads; a.G = c->cfg.n_kv_heads;
         a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
         a.general = L.attn_general;
         { Timed t(c, "attn_decode"); launch_attn_decode(a, S, p, s); }

@@ -7,14 +7,15 @@
 // running max strictly increases (a "record"), rescales the running sum S and
 // the value accumulator with a rounded factor (attention.rs:205-276).  Between
 // records every weight uses the same max, so a segment's contribution is a
-// plain integer sum (S in u64, vacc modulo 2^32) that can be formed in any
+// plain integer sum (S in u32, vacc modulo 2^32) that can be formed in any
 // order; only the rescales must be applied in key order.  Per tile the wave:
 //  1. forms S^T = K Q^T (int8 MFMA, K rows permuted so that each lane gets
 //     16 consecutive keys of its row) and the score epilogue in f64, which
 //     is exact: |dot / 4 * mult| < 2^49;
 //  2. scans its rows' keys in order (a lane owns 16 consecutive keys of one
-//     row): running max, records, one exp per key.  A key's weight and, at a
-//     record, the rescale factor are both E(-|s - max before the key|);
+//     row): running max, records, one exp per key from a table in LDS.  A
+//     key's weight and, at a record, the rescale factor are both
+//     E(-|s - max before the key|);
 //  3. for each segment index j = 0..max records, forms the segment sums of
 //     all 16 rows at once, O_j^T = V^T P_j^T, on int8 MFMA.  The 16-bit
 //     weights enter as two signed bytes: w - 32896 = 256*hi + lo, keys outside
@@ -24,77 +25,95 @@
 //  4. hands O_j through LDS to a "lanes = head dims" layout and walks each
 //     row's own segments: rescale at the record, then add (rows without a
 //     segment j skip the pass on a ballot bit); S is kept with lanes = rows.
-// INT32_MIN is the reference's "nothing seen yet" max (the fast path's scores
-// stay inside +-2^30, so no score equals it).
+//
+// Fast path (GEN false: |score| < 2^30 and lut[0] == 65535): scores are held
+// as score + 2^31 in a u32 (order-preserving), "nothing seen yet" is 0, and
+// the table step of a key is one multiply-add of |s - max|.  General path:
+// scores in i32 with the reference's wrapping differences, INT32_MIN for
+// "nothing seen yet".
 #pragma once
 
 #include "czip_device.h"
+#include "czip_kernels.h"
 
 namespace czip {
 
 constexpr unsigned WOFF = 32896;      // w - WOFF spans [-32896, 32639] = 256*[-128,127] + [-128,127]
+constexpr unsigned WB = 0x8080u;      // w ^ WB: the bytes of w - WOFF (each byte of w offset by 128)
 constexpr int RS = 68;                // row stride (words) of the per-wave buffer: 16-byte accesses of 16 rows hit 64 banks
 
 struct AttnWaveLds {
     unsigned buf[16][RS];    // per pass: the segment sums [row][dim]
-    uint16_t ex[16][72];     // [row][key]: at a record key, the rescale factor (0: nothing to rescale);
+    uint16_t ex[16][72];     // [row][key]: at a record key, the rescale factor ^ WB;
                              // 144-byte rows: 16-byte stores of 16 rows hit 64 banks
 };
 
 __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
+// The running max of a row before its first key: "nothing seen yet"
+// (INT32_MIN, attention.rs:205), and a max that no score passes (rows of a
+// decode wave that belong to no stream).
+template <bool GEN>
+__device__ __forceinline__ int attn_m_empty() { return GEN ? INT32_MIN : 0; }
+template <bool GEN>
+__device__ __forceinline__ int attn_m_never() { return GEN ? INT32_MAX : -1; }
+
 // sra_rne64(sra_rne32(dot, 2) * mult, 15) (attention.rs:233-239), mscale =
 // mult * 2^-15.  RNE of a quotient by 2^k is symmetric, so it is IEEE
-// round-half-even.  Fast path (|score| < 2^30, |mult| < 2^27), two FMAs
-// around B = 1.5 * 2^52 (ulp 1): r1 = fma(dot, 1/4, B) = B + du exactly
-// (du = sra_rne32(dot, 2)), and fma(r1, mscale, cb) with cb = B * (1 -
-// mscale) (exact: 1.5 * 2^37 * (2^15 - mult)) is B + du * mscale rounded
-// once, whose low word is the score.  The general path rounds du * mscale
-// in f64 (exact, |du * mult| < 2^49) and clamps to the i32 range.
-__device__ __forceinline__ double score_bias(double mscale) {
-    return __builtin_fma(-6755399441055744.0, mscale, 6755399441055744.0);
+// round-half-even.
+// Fast path (|score| < 2^30, |mult| < 2^27): r1 = dot + 1.5 * 2^54, whose
+// ulp is 4, is 1.5 * 2^54 + 4 du exactly (du = sra_rne32(dot, 2)); then
+// fma(r1, mscale / 4, cb) with cb = 1.5 * 2^52 + 2^31 - 1.5 * 2^52 * mscale
+// (exact: 1.5 * 2^37 * (2^15 - mult) + 2^31) is 1.5 * 2^52 + 2^31 +
+// du * mscale rounded once at ulp 1, whose low word is score + 2^31.
+// The general path rounds du * mscale in f64 (exact, |du * mult| < 2^49) and
+// clamps to the i32 range.
+__device__ __forceinline__ double score_bias_u(double mscale) {
+    return __builtin_fma(-6755399441055744.0, mscale, 6755399441055744.0 + 2147483648.0);
 }
-template <bool GEN>
-__device__ __forceinline__ int score_b(int dot, double mscale, double cb) {
-    if (!GEN) {
-        const double r1 = __builtin_fma((double)dot, 0.25, 6755399441055744.0);
-        return (int)(unsigned)__builtin_bit_cast(unsigned long long, __builtin_fma(r1, mscale, cb));
-    }
+__device__ __forceinline__ unsigned score_u(int dot, double ms4, double cbu) {
+    const double r1 = (double)dot + 27021597764222976.0;  // 1.5 * 2^54
+    return (unsigned)__builtin_bit_cast(unsigned long long, __builtin_fma(r1, ms4, cbu));
+}
+__device__ __forceinline__ int score_g(int dot, double mscale) {
     const int du = (dot + 1 + ((dot >> 2) & 1)) >> 2;
     double r = __builtin_rint((double)du * mscale);
     r = fmin(fmax(r, -2147483648.0), 2147483647.0);
     return (int)r;
 }
-
-// exp_q16(-neg) (lut.rs:213-235) with the table pre-shifted by 16 bits.
-// (65536 >> ip) * lut == (lut << 16) >> ip for ip <= 16, and both round to 0
-// (then clamp to 1) for ip >= 17; ip is capped at 31 like the reference's
-// early return.  neg == 0 reads lut[0], which the fast path requires to be 65535.
-__device__ __forceinline__ unsigned exp_neg(unsigned neg, const unsigned* lut32) {
-    const unsigned long long pr = (unsigned long long)neg * ATTN_COEF_Q24 + (1ull << 23);
-    const unsigned t = (unsigned)(pr >> 24);
-    const unsigned ip = min(t >> 8, 31u);
-    const unsigned x = ((lut32[t & 255u] >> ip) + 0x8000u) >> 16;
-    return max(x, 1u);
+// the row state's max after a sink of dot product `dot` (attention.rs:211-224)
+template <bool GEN>
+__device__ __forceinline__ int attn_sink_m(int dot, double mscale) {
+    if (GEN) return score_g(dot, mscale);
+    return (int)score_u(dot, mscale * 0.25, score_bias_u(mscale));
 }
 
-// The same for the fast path, with the table index from a difference d of
-// two scores held in f64: t = floor(|d| * coef / 2^24 + 1/2) is one FMA
-// (|d| < 2^32 and coef < 2^19, so the sum is exact) truncated to u32, and
-// t >= 17 * 256 (ip >= 17) always gives 1, so t is capped there.
-__device__ __forceinline__ unsigned exp_idx_f(double d) {
-    return (unsigned)fmin(__builtin_fma(fabs(d), (double)ATTN_COEF_Q24 * 0x1p-24, 0.5), 4352.0);
+// |a - b| of two u32 (v_sad_u32 with a zero accumulator)
+__device__ __forceinline__ unsigned absdiff_u32(unsigned a, unsigned b) {
+    unsigned r;
+    asm("v_sad_u32 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
 }
-// the value from the table word at t & 255
-__device__ __forceinline__ unsigned exp_from(unsigned t, unsigned word) {
-    return max(((word >> (t >> 8)) + 0x8000u) >> 16, 1u);
+
+// Table step of E(-n) (lut.rs:213-235): t = floor((n * coef + 2^23) / 2^24),
+// every step from 4096 on reading entry 4096.  Fast path: for every u32 n,
+// the high word of n * (coef * 2^8) + 2^31, one 32 x 32 + 64 multiply-add.
+__device__ __forceinline__ unsigned exp_step_u(unsigned n) {
+    const unsigned t = (unsigned)(((unsigned long long)n * (ATTN_COEF_Q24 << 8) + 0x80000000ull) >> 32);
+    return min(t, 4096u);
+}
+__device__ __forceinline__ unsigned exp_step_g(unsigned n) {
+    const unsigned long long t = ((unsigned long long)n * ATTN_COEF_Q24 + (1ull << 23)) >> 24;
+    return t < 4096ull ? (unsigned)t : 4096u;
 }
 
 // vacc rescale at a record (attention.rs:246-261): the low 32 bits of
-// ((i64)v * e + (v >= 0 ? 2^15 : -2^15)) >> 16 (one 32x32+64 multiply-add)
+// ((i64)v * e + (v >= 0 ? 2^15 : -2^15)) >> 16, written as
+// ((v * e + 2^15) >> 16) - (v < 0): for v < 0 the floor of (p + 2^15) / 2^16
+// less one is the floor of (p - 2^15) / 2^16.
 __device__ __forceinline__ unsigned rescale_v(unsigned v, unsigned e) {
-    const int c = (int)v >= 0 ? 0x8000 : -0x8000;
-    return (unsigned)(((long long)(int)v * (long long)(int)e + (long long)c) >> 16);
+    const long long p = (long long)(int)v * (long long)(int)e + 0x8000ll;  // e <= 65535
+    return (unsigned)(p >> 16) + (unsigned)((int)v >> 31);
 }
 
 // S rescale at a record (attention.rs:246-250): (S * e + 0x8000) >> 16.  S is
@@ -103,10 +122,6 @@ __device__ __forceinline__ unsigned rescale_v(unsigned v, unsigned e) {
 __device__ __forceinline__ unsigned rescale_s(unsigned S, unsigned e) {
     return (unsigned)(((unsigned long long)S * e + 0x8000ull) >> 16);
 }
-
-// bit 7 of each byte of the result: that byte of x is zero (exact per byte;
-// the other bits are junk)
-__device__ __forceinline__ unsigned zero_bytes_b7(unsigned x) { return ~(((x & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | x); }
 
 // selector of v_perm_b32 that spreads bit 7 of each byte of z over the byte:
 // perm(z, z << 8, .) with selectors 8..11 = sign bits 15 and 31 of the low
@@ -123,9 +138,9 @@ __device__ __forceinline__ unsigned pick(unsigned msk, unsigned a, unsigned b) {
 // row, the order of the scan, with no transpose.
 __device__ __forceinline__ int kperm(int blk, int m) { return 16 * (m >> 2) + 4 * blk + (m & 3); }
 
-// Running state of a wave's 16 rows: max m and weight sum S with
-// lanes = rows (replicated over the 4 lane groups); vacc with lanes = head
-// dims, register index = row.
+// Running state of a wave's 16 rows: max m (attn_m_empty / the scan's
+// representation) and weight sum S with lanes = rows (replicated over the 4
+// lane groups); vacc with lanes = head dims, register index = row.
 struct AttnRows {
     int m;
     unsigned S;
@@ -136,7 +151,7 @@ struct AttnRows {
 // head dims 16*(lane/16) .. +16; vop(s, db): the V^T operand of head dim
 // 16*db + lane%16, keys 16*(lane/16) .. +16 (each called once per index);
 // after_scan() runs once the scores have been scanned, before the V operands
-// are read.
+// are read.  etb: the exp table of attn_etab_host in LDS.
 // nvalid: keys [16*(lane/16), +nvalid) of the lane's row are visible (the
 // others get weight 0 and are never records), used when diag is set; rows
 // >= nrows are not combined into vacc (their m, S and vacc are unused).
@@ -151,88 +166,91 @@ struct AttnRows {
 // NS == 1: qs[0] is the query operand and rs is unused.
 template <bool GEN, int NS, class KOp, class VOp, class After>
 __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan, const v4i* qs, int rs, double mscale,
-                                          int nvalid, bool diag, int nrows, const unsigned* lut32, AttnWaveLds& W,
+                                          int nvalid, bool diag, int nrows, const uint16_t* etb, AttnWaveLds& W,
                                           AttnRows& st) {
     const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
 
     // 1. S^T = K Q^T and the score epilogue: lane (row, grp) gets the scores
     // of keys 16*grp .. +16 of its row (kperm)
-    int sv[16];
-    const double cb = score_bias(mscale);
+    unsigned sv[16];
+    {
+        const double ms4 = mscale * 0.25, cbu = score_bias_u(mscale);
 #pragma unroll
-    for (int blk = 0; blk < 4; blk++) {
-        v4i sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(0, blk), qs[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
+        for (int blk = 0; blk < 4; blk++) {
+            v4i sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(0, blk), qs[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-        for (int t = 1; t < NS; t++) sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(t, blk), qs[t], sc, 0, 0, 0);
+            for (int t = 1; t < NS; t++) sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(t, blk), qs[t], sc, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; i++) sv[blk * 4 + i] = score_b<GEN>(sc[i], mscale, cb);
+            for (int i = 0; i < 4; i++)
+                sv[blk * 4 + i] = GEN ? (unsigned)score_g(sc[i], mscale) : score_u(sc[i], ms4, cbu);
+        }
     }
 
     // 2. in-order scan of keys [16*grp, 16*grp+16) of this row
     if (diag) {
 #pragma unroll
         for (int k = 0; k < 16; k++)
-            if (k >= nvalid) sv[k] = INT32_MIN;  // never a record; weight masked below
+            if (k >= nvalid) sv[k] = (unsigned)attn_m_empty<GEN>();  // never a record; weight masked below
     }
-    int bmax = INT32_MIN;
+    // the running max entering this lane's keys: the row's max so far and the
+    // maxima of the lanes before it
+    auto vmax = [](unsigned a, unsigned b) { return GEN ? (unsigned)max((int)a, (int)b) : max(a, b); };
+    unsigned bmax = sv[0];
 #pragma unroll
-    for (int k = 0; k < 16; k++) bmax = max(bmax, sv[k]);
-    const int e1 = __shfl(bmax, (lane - 16) & 63, 64), e2 = __shfl(bmax, (lane - 32) & 63, 64),
-              e3 = __shfl(bmax, (lane - 48) & 63, 64);
-    int cur0 = st.m;
-    if (grp >= 1) cur0 = max(cur0, e1);
-    if (grp >= 2) cur0 = max(cur0, e2);
-    if (grp >= 3) cur0 = max(cur0, e3);
-    // weights and rescale factors: one exp per key, no branches, so the
-    // 16 table reads can be in flight together
+    for (int k = 1; k < 16; k++) bmax = vmax(bmax, sv[k]);
+    const unsigned e1 = (unsigned)__shfl((int)bmax, (lane - 16) & 63, 64),
+                   e2 = (unsigned)__shfl((int)bmax, (lane - 32) & 63, 64),
+                   e3 = (unsigned)__shfl((int)bmax, (lane - 48) & 63, 64);
+    unsigned cur0 = (unsigned)st.m;
+    if (grp >= 1) cur0 = vmax(cur0, e1);
+    if (grp >= 2) cur0 = vmax(cur0, e2);
+    if (grp >= 3) cur0 = vmax(cur0, e3);
+    // weights (offset bytes, WB) and rescale factors (^ WB): one exp per key,
+    // no branches, so the 16 table reads can be in flight together
     unsigned xs[16], ws[16];  // rescale factor (or weight) of each key, and its weight (65535 at a record)
     unsigned recm = 0u;   // bit k: key k is a record
     unsigned fresh = 0u;  // bit k: key k is a record over "nothing seen": no rescale, no split
-    int M = cur0;
     if (GEN) {
+        int M = (int)cur0;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            const int s = sv[k];
+            const int s = (int)sv[k];
             const bool rec = s > M;
             const int d = (int)(rec ? (unsigned)M - (unsigned)s : (unsigned)s - (unsigned)M);  // i32 wrap, as the reference
-            unsigned x = d >= 0 ? 65535u : exp_neg(0u - (unsigned)d, lut32);
-            ws[k] = rec ? 65535u : x;
-            const bool f = rec && M == INT32_MIN;  // a record over "nothing seen" has no rescale
-            x = f ? 0u : x;
-            fresh |= (f ? 1u : 0u) << k;
-            xs[k] = x;
+            const unsigned x = d >= 0 ? 65535u : ((unsigned)etb[exp_step_g(0u - (unsigned)d)] ^ WB);
+            ws[k] = (rec ? 65535u : x) ^ WB;
+            xs[k] = x ^ WB;
+            fresh |= (rec && M == INT32_MIN ? 1u : 0u) << k;
             recm |= (rec ? 1u : 0u) << k;
             M = max(M, s);
         }
     } else {
         // three phases, so that the 16 table reads are in flight together:
-        // the running max (f64) and every key's table index, the reads, the
-        // values.  Only the lane's first key can meet M == INT32_MIN as a
+        // the running max and every key's table step, the reads, the
+        // weights.  Only the lane's first key can meet "nothing seen" as a
         // record (masked keys are a suffix).
         unsigned tk[16];
         bool recb[16];
-        double Mf = (double)cur0;
+        unsigned M = cur0;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            const double sf = (double)sv[k];
-            recb[k] = sf > Mf;
-            tk[k] = exp_idx_f(Mf - sf);
-            Mf = fmax(Mf, sf);
+            const unsigned s = sv[k];
+            recb[k] = s > M;
+            tk[k] = exp_step_u(absdiff_u32(s, M));
+            M = max(M, s);
             recm |= (recb[k] ? 1u : 0u) << k;
         }
-        fresh = recb[0] && cur0 == INT32_MIN ? 1u : 0u;
+        fresh = recb[0] && cur0 == 0u ? 1u : 0u;
         __builtin_amdgcn_sched_barrier(0);
-        unsigned word[16];
+        unsigned eb[16];
 #pragma unroll
-        for (int k = 0; k < 16; k++) word[k] = lut32[tk[k] & 255u];
+        for (int k = 0; k < 16; k++) eb[k] = etb[tk[k]];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            const unsigned x = exp_from(tk[k], word[k]);
-            ws[k] = recb[k] ? 65535u : x;
-            xs[k] = k == 0 && fresh ? 0u : x;
+            ws[k] = recb[k] ? 0x7F7Fu : eb[k];  // a record's weight E(0) = 65535
+            xs[k] = eb[k];
         }
-        M = max(cur0, bmax);
     }
     // segments split at the records that rescale (a record over "nothing
     // seen" has nothing before it to rescale, so its segment runs on): the
@@ -248,41 +266,44 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
     // every key's factor, read at its split's pass
     {
         uint4 e0, e1v;
-        e0.x = xs[0] | (xs[1] << 16); e0.y = xs[2] | (xs[3] << 16); e0.z = xs[4] | (xs[5] << 16); e0.w = xs[6] | (xs[7] << 16);
-        e1v.x = xs[8] | (xs[9] << 16); e1v.y = xs[10] | (xs[11] << 16); e1v.z = xs[12] | (xs[13] << 16);
-        e1v.w = xs[14] | (xs[15] << 16);
+        e0.x = __builtin_amdgcn_perm(xs[1], xs[0], 0x05040100u); e0.y = __builtin_amdgcn_perm(xs[3], xs[2], 0x05040100u);
+        e0.z = __builtin_amdgcn_perm(xs[5], xs[4], 0x05040100u); e0.w = __builtin_amdgcn_perm(xs[7], xs[6], 0x05040100u);
+        e1v.x = __builtin_amdgcn_perm(xs[9], xs[8], 0x05040100u); e1v.y = __builtin_amdgcn_perm(xs[11], xs[10], 0x05040100u);
+        e1v.z = __builtin_amdgcn_perm(xs[13], xs[12], 0x05040100u); e1v.w = __builtin_amdgcn_perm(xs[15], xs[14], 0x05040100u);
         *(uint4*)&W.ex[row][grp * 16] = e0;
         *(uint4*)&W.ex[row][grp * 16 + 8] = e1v;
     }
-    // weights as signed byte pairs (a record's weight is 65535) and segment
-    // ids (splits up to and including the key); byte k of a dword = key
-    // 16*grp + 4*i + k
-    unsigned hi_dw[4], lo_dw[4], sg_dw[4];
+    // weights as signed byte pairs (the bytes of w ^ WB) and segment bytes
+    // dd = 128 + the key's segment id (splits up to and including the key,
+    // <= 64): byte k of a dword = key 16*grp + 4*i + k.  Pass j keeps
+    // dd - j * 0x01010101, whose bytes never borrow (63 <= 128 + id - j <= 192),
+    // so bit 7 of a byte tells id >= j.
+    unsigned hi_dw[4], lo_dw[4], dd[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const unsigned* w4 = ws + i * 4;
         const unsigned p01 = __builtin_amdgcn_perm(w4[1], w4[0], 0x05010400u);
         const unsigned p23 = __builtin_amdgcn_perm(w4[3], w4[2], 0x05010400u);
-        lo_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;
-        hi_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
+        lo_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+        hi_dw[i] = __builtin_amdgcn_perm(p23, p01, 0x07060302u);
         const unsigned nib = (splm >> (4 * i)) & 15u;
         const unsigned ones = (nib * 0x204081u) & 0x01010101u;  // bit k of nib -> byte k
         const unsigned base = seg + (unsigned)__builtin_popcount(splm & ((1u << (4 * i)) - 1u));
-        sg_dw[i] = (ones + base) * 0x01010101u;  // byte k: base + bits 0..k of nib (all < 256)
+        dd[i] = (ones + base) * 0x01010101u + 0x80808080u;  // byte k: 128 + base + bits 0..k of nib
     }
-    if (diag) {  // invisible keys: weight 0 (bytes 0x80), no segment (0xFF)
+    if (diag) {  // invisible keys: weight 0 (bytes 0x80), in no segment (id 127: bit 7 stays set)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int q = nvalid - 4 * i;
             const unsigned vm = q >= 4 ? 0xFFFFFFFFu : (q <= 0 ? 0u : ((1u << (8 * q)) - 1u));
             hi_dw[i] = pick(vm, hi_dw[i], 0x80808080u);
             lo_dw[i] = pick(vm, lo_dw[i], 0x80808080u);
-            sg_dw[i] = pick(vm, sg_dw[i], 0xFFFFFFFFu);
+            dd[i] = pick(vm, dd[i], 0xFFFFFFFFu);
         }
     }
     {
-        const int mr = max(M, __shfl_xor(M, 16, 64));
-        st.m = max(mr, __shfl_xor(mr, 32, 64));
+        const unsigned mr = vmax(vmax(cur0, bmax), (unsigned)__shfl_xor((int)vmax(cur0, bmax), 16, 64));
+        st.m = (int)vmax(mr, (unsigned)__shfl_xor((int)mr, 32, 64));
     }
 
     // 3. segment j of every row in pass j (MFMA column = row): O_j^T = V^T P_j^T
@@ -315,14 +336,15 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
 #pragma unroll
     for (int t = 0; t < NS; t++) sel[t] = NS == 1 || rs == t ? SEL_B7 : SEL_ZERO;
     for (int j = 0; j <= nmax; j++) {
-        const unsigned jb = (unsigned)j * 0x01010101u;
         v4i bhs[NS], bls[NS];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const unsigned z = zero_bytes_b7(sg_dw[i] ^ jb);
+            const unsigned dn = dd[i] - 0x01010101u;
+            const unsigned m = dd[i] & ~dn;  // bit 7 of a byte: id >= j and not id >= j + 1
+            dd[i] = dn;
 #pragma unroll
             for (int t = 0; t < NS; t++) {
-                const unsigned msk = spread_b7(z, sel[t]);
+                const unsigned msk = spread_b7(m, sel[t]);
                 bhs[t][i] = (int)pick(msk, hi_dw[i], 0x80808080u);
                 bls[t][i] = (int)pick(msk, lo_dw[i], 0x80808080u);
             }
@@ -342,7 +364,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
         unsigned erow = 0u;
         if (j >= 1) {
             const int key = rlo ? __builtin_ctz(rlo) : 32 + __builtin_ctz(rhi | 0x80000000u);
-            erow = j <= nrow ? (unsigned)W.ex[row][key] : 0u;
+            erow = j <= nrow ? (unsigned)W.ex[row][key] ^ WB : 0u;
             rhi = rlo ? rhi : rhi & (rhi - 1u);
             rlo &= rlo - 1u;
         }

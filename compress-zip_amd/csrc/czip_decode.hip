@@ -65,12 +65,12 @@ void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s) 
 // ---------------------------------------------------------------------------
 template <bool GEN, int NS>
 __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a, int p, int G) {
-    __shared__ unsigned lut32[256];
+    __shared__ __attribute__((aligned(16))) uint16_t etb[ETB_PAD];
     __shared__ __attribute__((aligned(16))) AttnWaveLds wl[4];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: streams, group and caches in SGPRs
     const int row = lane & 15, grp = lane >> 4;
-    lut32[tid] = (unsigned)a.lut[tid] << 16;
+    for (int i = tid; i < ETB_PAD / 8; i += 256) ((uint4*)etb)[i] = ((const uint4*)a.etab)[i];
     __syncthreads();
     const int item = (int)blockIdx.x * 4 + wave;
     const int sp = item / a.KH, g = item % a.KH;
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
     for (int t = 0; t < NS; t++) qs[t] = NS == 1 || rs == t ? qop : (v4i){0, 0, 0, 0};
 
     AttnRows st;
-    st.m = live ? INT32_MIN : INT32_MAX;  // dead rows: never a record
+    st.m = live ? attn_m_empty<GEN>() : attn_m_never<GEN>();  // dead rows: never a record
     st.S = 0;
     for (int r = 0; r < 16; r++) st.vacc[r] = 0;
     if (a.sink) {  // attention.rs:211-224: sink score is the initial max, weight E(0) = 65535
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
         dot += __shfl_xor(dot, 16, 64);
         dot += __shfl_xor(dot, 32, 64);
         if (live) {
-            st.m = score_b<GEN>(dot, mscale, score_bias(mscale));
+            st.m = attn_sink_m<GEN>(dot, mscale);
             st.S = 65535u;
         }
     }
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
                     kn[blk] = load_k(0, blk, tn);
                     return kc[blk];
                 },
-                [&](int, int db) { return vc[db]; }, [] {}, qs, 0, mscale, nvalid_at(t0), t0 + 63 > p, G, lut32,
+                [&](int, int db) { return vc[db]; }, [] {}, qs, 0, mscale, nvalid_at(t0), t0 + 63 > p, G, etb,
                 wl[wave], st);
 #pragma unroll
             for (int db = 0; db < 4; db++) vn[db] = load_v(0, db, tn);
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
 #pragma unroll
                         for (int blk = 0; blk < 4; blk++) kr[t][blk] = load_k(t, blk, tn);
                 },
-                qs, rs, mscale, nvalid_at(t0), t0 + 63 > p, NS * G, lut32, wl[wave], st);
+                qs, rs, mscale, nvalid_at(t0), t0 + 63 > p, NS * G, etb, wl[wave], st);
 #pragma unroll
             for (int t = 0; t < NS; t++)
 #pragma unroll

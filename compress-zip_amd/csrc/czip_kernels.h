@@ -36,6 +36,25 @@ struct GemmArgs {
     const int16_t* rsin;
 };
 
+// The attention's exp table by table step t (exp_q16, lut.rs:213-235):
+// E(t) = max(1, ((lut[t % 256] << 16 >> (t / 256)) + 2^15) >> 16) for
+// t < 4096, and entry 4096 stands for every larger step (a shift by 16 or more
+// leaves at most 1, which the clamp makes 1).  Entries hold E ^ 0x8080: the two
+// bytes of E each offset by 128, i.e. the signed byte pair (hi, lo) of
+// E - 32896 = 256 hi + lo that the PV products take.
+constexpr int ETB_N = 4097;    // entries used
+constexpr int ETB_PAD = 4104;  // entries allocated (whole 16-byte pieces)
+inline void attn_etab_host(const uint16_t* lut, uint16_t* out) {
+    for (int t = 0; t < ETB_PAD; t++) {
+        unsigned e = 1;
+        if (t < 4096) {
+            const unsigned x = ((((unsigned)lut[t & 255]) << 16 >> (t >> 8)) + 0x8000u) >> 16;
+            e = x < 1u ? 1u : x;
+        }
+        out[t] = (uint16_t)(e ^ 0x8080u);
+    }
+}
+
 struct AttnArgs {
     const int8_t* q;          // [M, H*64]  rotated + NET_SHIFT-ed queries
     const int8_t* kc;         // [B, KH, T, 64]
@@ -45,6 +64,7 @@ struct AttnArgs {
     const int32_t* score_mult;// [H]
     const int8_t* sink;       // [64] or nullptr
     const uint16_t* lut;      // [256]
+    const uint16_t* etab;     // [ETB_PAD]: E(t) ^ 0x8080 by table step t (attn_etab_host)
     int8_t* out;              // [M, H*64]
     int M, T, H, G, KH, kv_mode;
     unsigned coef;
