@@ -90,7 +90,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void k_attention(AttnArgs a) {
         int nvalid = p - (t0 + grp * 16) + 1;  // keys t <= p are visible (causal)
         nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
         attn_tile<GEN, 1>([&](int, int blk) { return kc[blk]; }, [&](int, int db) { return vc[db]; }, [] {}, &qop, 0,
-                          mscale, nvalid, t0 + 63 > wrow0, 16, etb, W, st);
+                          mscale, nvalid, t0 + 63 > wrow0, etb, W, st);
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) kc[blk] = load_k(blk, tn);
     }

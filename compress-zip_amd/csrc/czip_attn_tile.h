@@ -22,9 +22,9 @@
 //     segment j carry w = 0, and the constant 32896 * sum(v) (rows of ones
 //     times V) is added back; each row's weight sum for S comes from rows of
 //     ones times the weight columns;
-//  4. hands O_j through LDS to a "lanes = head dims" layout and walks each
-//     row's own segments: rescale at the record, then add (rows without a
-//     segment j skip the pass on a ballot bit); S is kept with lanes = rows.
+//  4. hands O_j through LDS to a "lanes = head dims" layout and adds it to
+//     every row, the rows whose record j falls in this pass rescaled first (a
+//     row without a segment j adds exactly 0); S is kept with lanes = rows.
 //
 // Fast path (GEN false: |score| < 2^30 and lut[0] == 65535): scores are held
 // as score + 2^31 in a u32 (order-preserving), "nothing seen yet" is 0, and
@@ -153,8 +153,8 @@ struct AttnRows {
 // after_scan() runs once the scores have been scanned, before the V operands
 // are read.  etb: the exp table of attn_etab_host in LDS.
 // nvalid: keys [16*(lane/16), +nvalid) of the lane's row are visible (the
-// others get weight 0 and are never records), used when diag is set; rows
-// >= nrows are not combined into vacc (their m, S and vacc are unused).
+// others get weight 0 and are never records), used when diag is set.  Every
+// row of the wave is combined into vacc; the caller reads only its own rows.
 //
 // NS > 1 packs NS independent key streams (decode: streams sharing nothing
 // but the shape) into the wave's rows (rs: the lane's row's stream, NS for
@@ -166,7 +166,7 @@ struct AttnRows {
 // NS == 1: qs[0] is the query operand and rs is unused.
 template <bool GEN, int NS, class KOp, class VOp, class After>
 __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan, const v4i* qs, int rs, double mscale,
-                                          int nvalid, bool diag, int nrows, const uint16_t* etb, AttnWaveLds& W,
+                                          int nvalid, bool diag, const uint16_t* etb, AttnWaveLds& W,
                                           AttnRows& st) {
     const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
 
@@ -371,34 +371,45 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
         // 4a. S of this lane's row (lanes = rows): rescale at record j, then add segment j
         if (erow) st.S = rescale_s(st.S, erow);
         st.S += (unsigned)sw + 64u * WOFF;
+        // the high- and low-byte products of two head-dim blocks at a time are
+        // independent, so their MFMAs issue back to back and one shift-add
+        // joins them
 #pragma unroll
-        for (int db = 0; db < 4; db++) {
-            v4i acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[0][db], bhs[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
+        for (int d2 = 0; d2 < 4; d2 += 2) {
+            v4i ah[2], al[2];
 #pragma unroll
-            for (int t = 1; t < NS; t++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[t][db], bhs[t], acc, 0, 0, 0);
-            acc = acc << 8;
+            for (int u = 0; u < 2; u++) {
+                ah[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[0][d2 + u], bhs[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
+                al[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[0][d2 + u], bls[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-            for (int t = 0; t < NS; t++) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[t][db], bls[t], acc, 0, 0, 0);
-            *(int4*)&W.buf[row][db * 16 + grp * 4] = make_int4(acc[0], acc[1], acc[2], acc[3]);
-        }
-        // rows (bit r, from lane r) that have a segment j, and those that
-        // rescale first
-        const unsigned long long live = __builtin_amdgcn_ballot_w64(j <= nrow);
-        const unsigned long long resc = __builtin_amdgcn_ballot_w64(erow != 0u);
-        wave_lds_fence();
-        // 4b. vacc (lanes = head dims): every row that has a segment j
-        unsigned bv[16];
+                for (int t = 1; t < NS; t++) {
+                    ah[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[t][d2 + u], bhs[t], ah[u], 0, 0, 0);
+                    al[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[t][d2 + u], bls[t], al[u], 0, 0, 0);
+                }
+            }
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-            if (r < nrows) bv[r] = W.buf[r][lane];
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            if (r < nrows && ((live >> r) & 1ull)) {
-                if ((resc >> r) & 1ull)
-                    st.vacc[r] = rescale_v(st.vacc[r], (unsigned)__builtin_amdgcn_readlane((int)erow, r));
-                st.vacc[r] += bv[r] + corr;
+            for (int u = 0; u < 2; u++) {
+                const v4i acc = (ah[u] << 8) + al[u];
+                *(int4*)&W.buf[row][(d2 + u) * 16 + grp * 4] = make_int4(acc[0], acc[1], acc[2], acc[3]);
             }
         }
+        // rows (bit r, from lane r) that rescale at record j (none in pass 0)
+        const unsigned long long resc = __builtin_amdgcn_ballot_w64(erow != 0u);
+        wave_lds_fence();
+        // 4b. vacc (lanes = head dims).  Every row adds: a row without a
+        // segment j has w = 0 (bytes -128) in every column, so its product is
+        // exactly -corr and it adds 0.
+        unsigned bv[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) bv[r] = W.buf[r][lane];
+        if (resc) {
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                if ((resc >> r) & 1ull)
+                    st.vacc[r] = rescale_v(st.vacc[r], (unsigned)__builtin_amdgcn_readlane((int)erow, r));
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) st.vacc[r] += bv[r] + corr;
         wave_lds_fence();
     }
 }

@@ -150,7 +150,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
                     kn[blk] = load_k(0, blk, tn);
                     return kc[blk];
                 },
-                [&](int, int db) { return vc[db]; }, [] {}, qs, 0, mscale, nvalid_at(t0), t0 + 63 > p, G, etb,
+                [&](int, int db) { return vc[db]; }, [] {}, qs, 0, mscale, nvalid_at(t0), t0 + 63 > p, etb,
                 wl[wave], st);
 #pragma unroll
             for (int db = 0; db < 4; db++) vn[db] = load_v(0, db, tn);
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
 #pragma unroll
                         for (int blk = 0; blk < 4; blk++) kr[t][blk] = load_k(t, blk, tn);
                 },
-                qs, rs, mscale, nvalid_at(t0), t0 + 63 > p, NS * G, etb, wl[wave], st);
+                qs, rs, mscale, nvalid_at(t0), t0 + 63 > p, etb, wl[wave], st);
 #pragma unroll
             for (int t = 0; t < NS; t++)
 #pragma unroll
