@@ -21,7 +21,10 @@ using namespace czip;
 namespace {
 
 constexpr uint32_t BOS = 1022u;  // main.rs:222, 387
-constexpr int FFN_MIN_ROWS = 1 << 19;  // rows from which a layer's FFN runs as one fused kernel
+constexpr int FFN_MIN_ROWS = 1 << 19;
+// V^T block exponent of the decode caches (vt_off): a step appends one key, whose 64 value
+// bytes span 256 bytes with 4-key blocks (1 KB with the prefill caches' 16-key blocks)
+constexpr int DEC_VL = 2;  // rows from which a layer's FFN runs as one fused kernel
 
 struct DevLayer {
     int8_t *attn_norm = nullptr, *post_attn_norm = nullptr, *ffn_norm = nullptr, *post_ffn_norm = nullptr;
@@ -575,7 +578,7 @@ void layer0_qkv(czip_ctx* c, GemmArgs& g, const uint32_t* tok, hipStream_t s) {
     const long long items = (long long)g.M * (8 * c->cfg.n_heads + 24 * NG);
     if (getenv("CZIP_QKV_GEMM") == nullptr && items < (1ll << 31)) {
         QkvTabArgs q{};
-        q.tab = c->qkv_tab; q.tok = tok; q.M = g.M; q.T = g.T; q.TP = g.TP; q.pos = g.pos;
+        q.tab = c->qkv_tab; q.tok = tok; q.M = g.M; q.T = g.T; q.TP = g.TP; q.pos = g.pos; q.vl = g.vl;
         q.H = c->cfg.n_heads; q.NG = NG; q.KH = c->KH; q.d = c->cfg.d_model; q.qkv_n = L.qkv_n;
         q.rcos = c->rcos; q.rsin = c->rsin; q.q8 = g.out8; q.kc = g.kc; q.vc = g.vc;
         Timed t(c, "qkv_table");
@@ -982,7 +985,7 @@ static czip_status run_decompress(czip_job* j) {
                 GemmArgs g{};
                 g.A = j->xn; g.W = L.qkv_w; g.M = S; g.N = L.qkv_n; g.K = d;
                 g.out8 = j->q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
-                g.d = d; g.T = TP; g.TP = TP; g.pos = p; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
+                g.d = d; g.T = TP; g.TP = TP; g.pos = p; g.vl = DEC_VL; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
                 g.KH = c->KH; g.kc = kc; g.vc = vc; g.rcos = c->rcos; g.rsin = c->rsin;
                 if (l == 0) {
                     layer0_qkv(c, g, j->inp, s);
@@ -991,7 +994,7 @@ static czip_status run_decompress(czip_job* j) {
                     launch_gemm(g, EPI_QKV, s);
                 }
                 AttnArgs a{};
-                a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = j->d_ntok + g0; a.score_mult = L.score_mult;
+                a.q = j->q8; a.kc = kc; a.vc = vc; a.vl = DEC_VL; a.TP = TP; a.lens = j->d_ntok + g0; a.score_mult = L.score_mult;
                 a.sink = L.sink; a.lut = c->lut; a.etab = c->etab; a.out = j->attn; a.M = S; a.T = TP; a.H = H; a.G = c->cfg.n_kv_heads;
                 a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;
                 a.general = L.attn_general;
@@ -1136,7 +1139,7 @@ extern "C" czip_status czip_decode_step(czip_ctx* c, const uint32_t* tok_in, con
         GemmArgs g{};
         g.A = j->xn; g.W = L.qkv_w; g.M = S; g.N = L.qkv_n; g.K = d;
         g.out8 = j->q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
-        g.d = d; g.T = TP; g.TP = TP; g.pos = p; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
+        g.d = d; g.T = TP; g.TP = TP; g.pos = p; g.vl = DEC_VL; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
         g.KH = c->KH; g.kc = kc; g.vc = vc; g.rcos = c->rcos; g.rsin = c->rsin;
         if (l == 0) {
             layer0_qkv(c, g, j->inp, s);
@@ -1145,7 +1148,7 @@ extern "C" czip_status czip_decode_step(czip_ctx* c, const uint32_t* tok_in, con
             launch_gemm(g, EPI_QKV, s);
         }
         AttnArgs a{};
-        a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = j->d_ntok; a.score_mult = L.score_mult;
+        a.q = j->q8; a.kc = kc; a.vc = vc; a.vl = DEC_VL; a.TP = TP; a.lens = j->d_ntok; a.score_mult = L.score_mult;
         a.sink = L.sink; a.lut = c->lut; a.etab = c->etab; a.out = j->attn; a.M = S; a.T = TP; a.H = c->cfg.n_heads; a.G = c->cfg.n_kv_heads;
         a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
         a.general = L.attn_general;

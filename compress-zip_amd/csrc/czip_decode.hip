@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
 
     const int ntiles = p / 64 + 1;  // keys 0..p; tile t0 + 64 <= p stays inside TP
     // buffer loads: one 32-bit offset per lane, range-checked against the
-    // stream's TP * 64 bytes of K ([TP][64]) and of V^T ([TP/16][64][16])
+    // stream's TP * 64 bytes of K ([TP][64]) and of V^T (vt_off)
     __amdgpu_buffer_rsrc_t rk[NS], rv[NS];
 #pragma unroll
     for (int t = 0; t < NS; t++) {
@@ -132,8 +132,15 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
     auto load_k = [&](int t, int blk, int t0) {
         return __builtin_amdgcn_raw_buffer_load_b128(rk[t], (t0 + kperm(blk, row)) * 64 + grp * 16, 0, 0);
     };
+    // V^T (vt_off): the operand's 16 keys of one dim are one 16-byte word in
+    // 16-key blocks, four 4-byte words 256 bytes apart in 4-key blocks
     auto load_v = [&](int t, int db, int t0) {
-        return __builtin_amdgcn_raw_buffer_load_b128(rv[t], ((t0 / 16 + grp) * 64 + db * 16 + row) * 16, 0, 0);
+        const int o = vt_off(t0 + grp * 16, db * 16 + row, a.vl);
+        if (a.vl == 4) return __builtin_amdgcn_raw_buffer_load_b128(rv[t], o, 0, 0);
+        return (v4i){(int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o, 0, 0),
+                     (int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o + 256, 0, 0),
+                     (int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o + 512, 0, 0),
+                     (int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o + 768, 0, 0)};
     };
     auto nvalid_at = [&](int t0) {
         const int n = p - (t0 + grp * 16) + 1;

@@ -27,6 +27,16 @@ __device__ __forceinline__ int clamp127(int x) { return x < -127 ? -127 : (x > 1
 // 4 extra cycles per read and 8 per store).
 __device__ __forceinline__ int lds64(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
 
+// V^T caches hold each KV head's values transposed in blocks of 2^vl keys,
+// [key >> vl][dim][key & (2^vl - 1)]: the PV operand (16 consecutive keys of
+// one dim) is one 16-byte load with 16-key blocks (vl = 4, the prefill
+// caches) and four 4-byte loads with 4-key blocks (vl = 2, the caches a
+// decode step appends one key to: the step's 64 value bytes then fall in 256
+// bytes instead of 1 KB).  Byte offset of (key p, dim) in a head's cache:
+__device__ __forceinline__ int vt_off(int p, int dim, int vl) {
+    return ((p >> vl) << (6 + vl)) + (dim << vl) + (p & ((1 << vl) - 1));
+}
+
 constexpr int BUF_DWORD3 = 0x00020000;  // word 3 of a raw buffer resource: 32-bit data format, no swizzle
 
 // Fragment-major weights: for W [N, K] (N % 16 == 0, K % 64 == 0) the MFMA

@@ -143,13 +143,13 @@ __device__ __forceinline__ void epi_tile(const GemmArgs& a, const v4i* acc, int 
                 *(unsigned*)(k + i0) = pack4i(xq[0], xq[1], xq[2], xq[3]);
                 *(unsigned*)(k + i0 + 32) = pack4i(yq[0], yq[1], yq[2], yq[3]);
             } else {
-                // V^T in blocks of 16 keys, [key/16][dim][16]: the PV operand
-                // of both attention kernels is 16 consecutive keys of one dim
-                int8_t* v = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP + (size_t)(p >> 4) * 1024 + (p & 15);
+                // V^T in blocks of 2^vl keys (vt_off)
+                const int vl = a.vl;
+                int8_t* v = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP + vt_off(p, 0, vl);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    v[(i0 + r) * 16] = (int8_t)xv[r];
-                    v[(i0 + r + 32) * 16] = (int8_t)yv[r];
+                    v[(i0 + r) << vl] = (int8_t)xv[r];
+                    v[(i0 + r + 32) << vl] = (int8_t)yv[r];
                 }
             }
         }
@@ -243,6 +243,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
 struct WsOut {
     __amdgpu_buffer_rsrc_t o;      // out8 / out32 from the strip's first row r0
     __amdgpu_buffer_rsrc_t k, v;   // QKV: K / V^T caches from chunk b0
+    int vl;                        // QKV: the V^T block exponent (vt_off)
     int r0, b0;
 };
 
@@ -341,7 +342,7 @@ __device__ __forceinline__ void epi_ws(const GemmArgs& a, const WsOut& ro, const
         if (ROLE != 2) transpose4(t.d);
         if (ROLE == 0) t.off = (row - ro.r0) * a.ldo + col_base + c4 * 4;
         else if (ROLE == 1) t.off = valid ? ((bl * a.KH + g) * a.T + p) * 64 + c4 * 4 : (int)0xFFFFFF00u;
-        else t.off = valid ? (bl * a.KH + g) * 64 * a.TP + (p >> 4) * 1024 + (p & 15) + c4 * 16 : (int)0xFFFF0000u;
+        else t.off = valid ? (bl * a.KH + g) * 64 * a.TP + vt_off(p, c4, a.vl) : (int)0xFFFF0000u;
     }
 }
 
@@ -354,15 +355,15 @@ __device__ __forceinline__ void flush_ws(const WsOut& ro, const WsTile& t) {
     } else if (EPI == EPI_REGLU) {
         __builtin_amdgcn_raw_buffer_store_b64((v2i){(int)t.d[0], (int)t.d[1]}, ro.o, t.off, 0, 0);
     } else if (EPI == EPI_QKV) {
-        // V^T in blocks of 16 keys, [key/16][dim][16]: dim i is at byte 16 i
+        // V^T in blocks of 2^vl keys (vt_off): dim i of the key is at byte i << vl
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 __builtin_amdgcn_raw_buffer_store_b8((unsigned char)(t.d[2 * j] >> (8 * r)), ro.v,
-                                                     t.off + (j * 16 + r) * 16, 0, 0);
+                                                     t.off + ((j * 16 + r) << ro.vl), 0, 0);
                 __builtin_amdgcn_raw_buffer_store_b8((unsigned char)(t.d[2 * j + 1] >> (8 * r)), ro.v,
-                                                     t.off + (j * 16 + r + 32) * 16, 0, 0);
+                                                     t.off + ((j * 16 + r + 32) << ro.vl), 0, 0);
             }
     }
 }
@@ -502,6 +503,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_ws(GemmArgs a, int ncg) {
                                                      (int)min((nb - ro.b0) * kb, 0x7FFFFFFFll), BUF_DWORD3);
             ro.v = __builtin_amdgcn_make_buffer_rsrc((void*)(a.vc + ro.b0 * vb), (short)0,
                                                      (int)min((nb - ro.b0) * vb, 0x7FFFFFFFll), BUF_DWORD3);
+            ro.vl = a.vl;
         }
         WsTile t[NT];
         if (wlive) {

@@ -30,7 +30,8 @@ struct GemmArgs {
     int d, T, kv_mode, G, KH;
     int TP;           // keys per V^T block: T rounded up to a multiple of 64
     int8_t* kc;       // [B, KH, T, 64]   rotated keys
-    int8_t* vc;       // [B, KH, TP/16, 64, 16]  values, transposed in blocks of 16 keys
+    int8_t* vc;       // [B, KH, TP * 64] values, transposed in blocks of 2^vl keys (vt_off)
+    int vl = 4;       // V^T block exponent: 4 for the prefill caches, 2 for the decode caches
     int pos;          // >= 0: every row is at this position and row = chunk (decode step)
     const int16_t* rcos;
     const int16_t* rsin;
@@ -58,7 +59,8 @@ inline void attn_etab_host(const uint16_t* lut, uint16_t* out) {
 struct AttnArgs {
     const int8_t* q;          // [M, H*64]  rotated + NET_SHIFT-ed queries
     const int8_t* kc;         // [B, KH, T, 64]
-    const int8_t* vc;         // [B, KH, TP/16, 64, 16]
+    const int8_t* vc;         // [B, KH, TP * 64] values transposed in blocks of 2^vl keys (vt_off)
+    int vl = 4;
     int TP;
     const int32_t* lens;      // [B]
     const int32_t* score_mult;// [H]
@@ -151,7 +153,8 @@ struct QkvTabArgs {
     const int16_t* rsin;
     int8_t* q8;              // [M, d]
     int8_t* kc;              // [B, KH, T, 64]
-    int8_t* vc;              // [B, KH, TP/16, 64, 16]
+    int8_t* vc;              // [B, KH, TP * 64] values transposed in blocks of 2^vl keys (vt_off)
+    int vl = 4;
 };
 void launch_qkv_table(const QkvTabArgs& a, hipStream_t s);
 

@@ -218,12 +218,13 @@ __global__ __launch_bounds__(256) void k_qkv_table(QkvTabArgs a) {
     const int row = idx / per_row, it = idx - row * per_row;
     const int b = a.pos >= 0 ? row : row / a.T, p = a.pos >= 0 ? a.pos : row - b * a.T;
     const int8_t* t = a.tab + (size_t)a.tok[row] * a.qkv_n;
-    if (it >= 8 * a.H + 8 * a.NG) {  // V: dims 4 q .. 4 q + 3 of head g, [key/16][dim][16]
+    if (it >= 8 * a.H + 8 * a.NG) {  // V: dims 4 q .. 4 q + 3 of head g, in blocks of 2^vl keys (vt_off)
         const int v = it - 8 * a.H - 8 * a.NG, g = v >> 4, q = v & 15;
         const unsigned w = *(const unsigned*)(t + a.d + 64 * a.NG + 64 * g + 4 * q);
-        int8_t* dst = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP + (size_t)(p >> 4) * 1024 + (p & 15) + 4 * q * 16;
+        const int vl = a.vl;
+        int8_t* dst = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP + vt_off(p, 4 * q, vl);
 #pragma unroll
-        for (int r = 0; r < 4; r++) dst[r * 16] = (int8_t)(w >> (8 * r));
+        for (int r = 0; r < 4; r++) dst[r << vl] = (int8_t)(w >> (8 * r));
         return;
     }
     const bool isq = it < 8 * a.H;
