@@ -21,10 +21,11 @@ using namespace czip;
 namespace {
 
 constexpr uint32_t BOS = 1022u;  // main.rs:222, 387
-constexpr int FFN_MIN_ROWS = 1 << 19;
+constexpr int FFN_MIN_ROWS = 1 << 19;  // rows from which a layer's FFN runs as one fused kernel
 // V^T block exponent of the decode caches (vt_off): a step appends one key, whose 64 value
-// bytes span 256 bytes with 4-key blocks (1 KB with the prefill caches' 16-key blocks)
-constexpr int DEC_VL = 2;  // rows from which a layer's FFN runs as one fused kernel
+// bytes span 256 bytes with 4-key blocks (1 KB with the prefill caches' 16-key blocks); the
+// decode attention reads this layout
+constexpr int DEC_VL = 2;
 
 struct DevLayer {
     int8_t *attn_norm = nullptr, *post_attn_norm = nullptr, *ffn_norm = nullptr, *post_ffn_norm = nullptr;
@@ -994,7 +995,7 @@ static czip_status run_decompress(czip_job* j) {
                     launch_gemm(g, EPI_QKV, s);
                 }
                 AttnArgs a{};
-                a.q = j->q8; a.kc = kc; a.vc = vc; a.vl = DEC_VL; a.TP = TP; a.lens = j->d_ntok + g0; a.score_mult = L.score_mult;
+                a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = j->d_ntok + g0; a.score_mult = L.score_mult;
                 a.sink = L.sink; a.lut = c->lut; a.etab = c->etab; a.out = j->attn; a.M = S; a.T = TP; a.H = H; a.G = c->cfg.n_kv_heads;
                 a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;
                 a.general = L.attn_general;
@@ -1148,7 +1149,7 @@ extern "C" czip_status czip_decode_step(czip_ctx* c, const uint32_t* tok_in, con
             launch_gemm(g, EPI_QKV, s);
         }
         AttnArgs a{};
-        a.q = j->q8; a.kc = kc; a.vc = vc; a.vl = DEC_VL; a.TP = TP; a.lens = j->d_ntok; a.score_mult = L.score_mult;
+        a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = j->d_ntok; a.score_mult = L.score_mult;
         a.sink = L.sink; a.lut = c->lut; a.etab = c->etab; a.out = j->attn; a.M = S; a.T = TP; a.H = c->cfg.n_heads; a.G = c->cfg.n_kv_heads;
         a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
         a.general = L.attn_general;

@@ -132,11 +132,10 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
     auto load_k = [&](int t, int blk, int t0) {
         return __builtin_amdgcn_raw_buffer_load_b128(rk[t], (t0 + kperm(blk, row)) * 64 + grp * 16, 0, 0);
     };
-    // V^T (vt_off): the operand's 16 keys of one dim are one 16-byte word in
-    // 16-key blocks, four 4-byte words 256 bytes apart in 4-key blocks
+    // V^T of the decode caches in 4-key blocks (vt_off, vl = 2): the operand's
+    // 16 keys of one dim are four 4-byte words, 256 bytes apart
     auto load_v = [&](int t, int db, int t0) {
-        const int o = vt_off(t0 + grp * 16, db * 16 + row, a.vl);
-        if (a.vl == 4) return __builtin_amdgcn_raw_buffer_load_b128(rv[t], o, 0, 0);
+        const int o = vt_off(t0 + grp * 16, db * 16 + row, 2);
         return (v4i){(int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o, 0, 0),
                      (int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o + 256, 0, 0),
                      (int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o + 512, 0, 0),

@@ -59,8 +59,8 @@ inline void attn_etab_host(const uint16_t* lut, uint16_t* out) {
 struct AttnArgs {
     const int8_t* q;          // [M, H*64]  rotated + NET_SHIFT-ed queries
     const int8_t* kc;         // [B, KH, T, 64]
-    const int8_t* vc;         // [B, KH, TP * 64] values transposed in blocks of 2^vl keys (vt_off)
-    int vl = 4;
+    const int8_t* vc;         // [B, KH, TP * 64] values transposed in blocks of keys (vt_off): 16 keys
+                              // for the prefill kernel, 4 for the decode kernel (caches a decode step appends to)
     int TP;
     const int32_t* lens;      // [B]
     const int32_t* score_mult;// [H]
