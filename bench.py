@@ -26,9 +26,9 @@ PEAK_HBM_GBS = 8000.0       # GB/s
 
 # HBM bytes per token (read + write) of each kernel on the text workload, from
 # two rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0: the factors a
-# plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text_1Mtok.md
-TRAFFIC_B_PER_TOKEN = {"attention": 523 + 405, "qkv_table": 13 + 512, "gemm_o_norm": 397 + 1152,
-                       "gemm_down_norm": 1814 + 384, "gemm_up": 556 + 1024, "head_cdf": 391 + 8}
+# plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text.md
+TRAFFIC_B_PER_TOKEN = {"attention": 516 + 411, "qkv_table": 12 + 512, "gemm_o_norm": 396 + 1152,
+                       "ffn": 1584 + 385, "gemm_down_norm": 1814 + 384, "gemm_up": 556 + 1024, "head_cdf": 390 + 8}
 TRAFFIC_WORKLOADS = ("v001_L4_ctx512_text64MiB",)
 # Prefill attention: wave64 VALU instructions (MFMA excluded) per 16-row x 64-key tile,
 # from SQ_INSTS_VALU - SQ_INSTS_VALU_MFMA_I8 on the same workload
