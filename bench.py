@@ -127,6 +127,7 @@ def cpu_baseline(model_path, tokens, chunk, budget_s=15.0, kv_mode=0, extra_chun
     dt = time.perf_counter() - t
     coded = dict(enumerate(first))
     extra = [c for c in extra_chunks if c not in coded]
+    log(f"cpu baseline: {k} chunks in {dt:.1f} s; coding {len(extra)} more for the parity sample")
     if extra:
         sample = np.concatenate([tokens[c * chunk:(c + 1) * chunk] for c in extra])
         # every extra chunk but the job's last is full, so chunk boundaries line up
@@ -193,6 +194,7 @@ def main():
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1000.0 / args.steps
     value = n / (ms / 1000.0)
+    log(f"compress: {ms:.1f} ms per step, {value / 1e6:.2f} M tok/s")
     # the per-kernel breakdown: one more step with HIP events around every launch
     model.reset_stats()
     model.set_profiling(True)
@@ -261,6 +263,7 @@ def main():
     if not args.no_decompress:
         ntoks = [min(chunk, n - c * chunk) for c in range(len(chunks))]
         djob = model.decompress_plan(chunks, ntoks)
+        log(f"decompress: {len(chunks)} streams ...")
         # the rate comes from a run without events (a decode job launches
         # ~7 kernels per step); the per-kernel times from a second run of the
         # same job with HIP events around every launch
@@ -272,6 +275,7 @@ def main():
             raise SystemExit("decompressed tokens differ from the input")
         if text is not None and tokenizer.decode_bytes(back) != text:
             raise SystemExit("detokenized output differs from the input text")
+        log(f"decompress: {(t1 - t0):.2f} s, {n / (t1 - t0) / 1e6:.3f} M tok/s, tokens identical; per-kernel run ...")
         model.reset_stats()
         model.set_profiling(True)
         djob.run()
