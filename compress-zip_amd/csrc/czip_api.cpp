@@ -921,6 +921,7 @@ extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t* data, co
     const double per_stream = (double)row_bytes(c, !c->head_fused) + 2.0 * L * (double)c->KH * pad64(Tcap) * 64 + 64;
     int64_t S = (int64_t)(gb * 1e9 / per_stream);
     if (const char* s = getenv("CZIP_DECODE_STREAMS")) S = std::min<int64_t>(S, atoll(s));
+    S = std::min<int64_t>(S, INT32_MAX / (int64_t)d);  // decode row offsets are 32-bit
     S = std::max<int64_t>(1, std::min<int64_t>(S, std::max(nchunks, 1)));
     j->S = (int)S;
     std::vector<int64_t> toff((size_t)std::max(nchunks, 1), 0);
@@ -1062,6 +1063,8 @@ static void free_decode_session(czip_ctx* c) {
 extern "C" czip_status czip_decode_begin(czip_ctx* c, int32_t S, int32_t T) {
     if (!c) return CZIP_E_ARG;
     if (S < 1 || T < 1) return fail(c, CZIP_E_ARG, "S and T must be >= 1");
+    if ((int64_t)S * c->cfg.d_model > INT32_MAX)
+        return fail(c, CZIP_E_RANGE, "S * d_model must stay below 2^31 (decode row offsets are 32-bit)");
     if (T > c->cfg.context_length || T > c->cfg.max_seq_len)
         return fail(c, CZIP_E_RANGE, "T exceeds the RoPE LUT / KV cache (lut.rs:169-177)");
     HIPCHECK(c, hipSetDevice(c->device));

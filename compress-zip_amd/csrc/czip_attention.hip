@@ -89,22 +89,16 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void k_attention(AttnArgs a) {
         for (int db = 0; db < 4; db++) vc[db] = load_v(db, t0);
         int nvalid = p - (t0 + grp * 16) + 1;  // keys t <= p are visible (causal)
         nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
-        attn_tile<GEN, 1>([&](int, int blk) { return kc[blk]; }, [&](int, int db) { return vc[db]; }, [] {}, &qop, 0,
+        attn_tile<GEN, 1>([&](int, int blk) { return kc[blk]; }, [&](int, int db) { return vc[db]; }, &qop, 0,
                           mscale, nvalid, t0 + 63 > wrow0, etb, W, st);
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) kc[blk] = load_k(blk, tn);
     }
 
-    // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const unsigned Sr = (unsigned)__shfl((int)st.S, r, 64);
-        const int pr = wrow0 + r;
-        if (pr < len) {
-            const unsigned long long den = Sr == 0u ? 1ull : (unsigned long long)Sr;
-            a.out[((size_t)b * T + pr) * D + h * 64 + lane] = (int8_t)clamp127(div_rne_s32_u64((int)st.vacc[r], den));
-        }
-    }
+    int8_t* const orow = a.out + ((size_t)b * T + wrow0) * D + h * 64;
+    attn_normalize(st, [&](int r, int8_t v) {
+        if (wrow0 + r < len) orow[(size_t)r * D + lane] = v;
+    });
 }
 
 void launch_attention(const AttnArgs& a, int B, hipStream_t s) {

@@ -149,9 +149,8 @@ struct AttnRows {
 
 // One 64-key tile.  kop(s, blk): the K operand of key kperm(blk, lane%16),
 // head dims 16*(lane/16) .. +16; vop(s, db): the V^T operand of head dim
-// 16*db + lane%16, keys 16*(lane/16) .. +16 (each called once per index);
-// after_scan() runs once the scores have been scanned, before the V operands
-// are read.  etb: the exp table of attn_etab_host in LDS.
+// 16*db + lane%16, keys 16*(lane/16) .. +16 (each called once per index,
+// the V operands after the scan).  etb: the exp table of attn_etab_host in LDS.
 // nvalid: keys [16*(lane/16), +nvalid) of the lane's row are visible (the
 // others get weight 0 and are never records), used when diag is set.  Every
 // row of the wave is combined into vacc; the caller reads only its own rows.
@@ -164,8 +163,8 @@ struct AttnRows {
 // reads stream s, else 0), the PV products with weight 0 in the other
 // streams' columns (a constant, corrected like the keys outside a segment).
 // NS == 1: qs[0] is the query operand and rs is unused.
-template <bool GEN, int NS, class KOp, class VOp, class After>
-__device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan, const v4i* qs, int rs, double mscale,
+template <bool GEN, int NS, class KOp, class VOp>
+__device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, int rs, double mscale,
                                           int nvalid, bool diag, const uint16_t* etb, AttnWaveLds& W,
                                           AttnRows& st) {
     const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
@@ -307,7 +306,6 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
     }
 
     // 3. segment j of every row in pass j (MFMA column = row): O_j^T = V^T P_j^T
-    after_scan();
     int nmax = nrow;
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
@@ -411,6 +409,41 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, After after_scan,
 #pragma unroll
         for (int r = 0; r < 16; r++) st.vacc[r] += bv[r] + corr;
         wave_lds_fence();
+    }
+}
+
+__device__ __forceinline__ double bcast_f64(double x, int lane) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, x);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, lane);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), lane);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
+// Normalization (attention.rs:278-285): emit(r, clamp127(div_rne(vacc[r], S_r)))
+// for the 16 rows, lane = head dim, S = 0 read as 1 (div_rne of
+// primitives.rs:163-185: the quotient of |v| rounded half to even, then the
+// sign).  In f64 from one reciprocal per row (lanes = rows): q = rint(min(|v|
+// * (1/S), 128)) is the rounded quotient unless it is a tie, the estimate
+// being within 128.5 * 2^-52 of |v| / S while a quotient that is no tie lies
+// at least 1/(2S) >= 2^-33 from every half-integer; r2 = 2 (|v| - q S) is
+// exact (q S < 2^40) and equals +-S exactly at a tie, where the even
+// neighbour wins.  Quotients from 127.5 up give 127 (the clamp).
+template <class Emit>
+__device__ __forceinline__ void attn_normalize(const AttnRows& st, Emit emit) {
+    const double dl = (double)max(st.S, 1u);
+    const double il = 1.0 / dl;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const double inv = bcast_f64(il, r), den = bcast_f64(dl, r);
+        const int n = (int)st.vacc[r];
+        const unsigned an = n < 0 ? 0u - (unsigned)n : (unsigned)n;
+        const double af = (double)an;
+        const double q = __builtin_rint(__builtin_fmin(af * inv, 128.0));
+        const double r2 = 2.0 * __builtin_fma(-q, den, af);
+        unsigned qi = (unsigned)q;
+        const unsigned odd = __builtin_fabs(r2) == den ? (qi & 1u) : 0u;
+        qi = min(r2 > 0.0 ? qi + odd : qi - odd, 127u);
+        emit(r, (int8_t)(n < 0 ? -(int)qi : (int)qi));
     }
 }
 

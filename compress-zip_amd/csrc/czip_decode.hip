@@ -60,8 +60,9 @@ void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s) 
 // streams share a wavefront (rows [0, G) and [G, 2G)), each meeting only its
 // own stream's keys.  Each lane loads its own K and V^T operand fragments
 // (16 bytes each) straight from the caches, one tile ahead: one stream into
-// a second register set, two streams in place (the next K once the scores
-// are scanned, the next V after the tile's passes).
+// a second register set, two streams in place (the next K and V after the
+// tile's passes; the V latency is covered by the scores and the scan, the K
+// latency by the other waves of the SIMD).
 // ---------------------------------------------------------------------------
 template <bool GEN, int NS>
 __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a, int p, int G) {
@@ -156,8 +157,8 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
                     kn[blk] = load_k(0, blk, tn);
                     return kc[blk];
                 },
-                [&](int, int db) { return vc[db]; }, [] {}, qs, 0, mscale, nvalid_at(t0), t0 + 63 > p, etb,
-                wl[wave], st);
+                [&](int, int db) { return vc[db]; }, qs, 0, mscale, nvalid_at(t0), t0 + 63 > p, etb, wl[wave],
+                st);
 #pragma unroll
             for (int db = 0; db < 4; db++) vn[db] = load_v(0, db, tn);
         };
@@ -188,32 +189,33 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
         for (int kt = 0; kt < ntiles; kt++) {
             const int t0 = kt * 64;
             const int tn = t0 + 64 <= p ? t0 + 64 : t0;
-            attn_tile<GEN, NS>(
-                [&](int t, int blk) { return kr[t][blk]; }, [&](int t, int db) { return vr[t][db]; },
-                [&] {
+            attn_tile<GEN, NS>([&](int t, int blk) { return kr[t][blk]; }, [&](int t, int db) { return vr[t][db]; },
+                               qs, rs, mscale, nvalid_at(t0), t0 + 63 > p, etb, wl[wave], st);
+            // the next tile's K and V once the passes are done: no operand
+            // register is live across the passes (168 VGPRs, three waves per
+            // SIMD; the next K requested after the scan held 210, two waves)
 #pragma unroll
-                    for (int t = 0; t < NS; t++)
+            for (int t = 0; t < NS; t++)
 #pragma unroll
-                        for (int blk = 0; blk < 4; blk++) kr[t][blk] = load_k(t, blk, tn);
-                },
-                qs, rs, mscale, nvalid_at(t0), t0 + 63 > p, etb, wl[wave], st);
+                for (int blk = 0; blk < 4; blk++) kr[t][blk] = load_k(t, blk, tn);
 #pragma unroll
             for (int t = 0; t < NS; t++)
 #pragma unroll
                 for (int db = 0; db < 4; db++) vr[t][db] = load_v(t, db, tn);
         }
     }
-    // normalize (attention.rs:278-285): lane = head dim; S of row r lives in lane r
+    // each lane forms the output offset of its row (-1: no live row), read
+    // per row into a scalar: out[S][H * 64] stays below 2^31 bytes (host check)
+    const int rs2 = NS == 1 ? 0 : (row >= G) + (row >= 2 * G);
+    bool live2 = row < NS * G;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const unsigned Sr = (unsigned)__shfl((int)st.S, r, 64);
-        const int t = NS == 1 ? 0 : r / G;
-        if (r < NS * G && act[t < NS ? t : 0]) {
-            const unsigned long long den = Sr == 0u ? 1ull : (unsigned long long)Sr;
-            a.out[(size_t)bs[t] * D + (h0 + r - t * G) * 64 + lane] =
-                (int8_t)clamp127(div_rne_s32_u64((int)st.vacc[r], den));
-        }
-    }
+    for (int t = 0; t < NS; t++)
+        if (rs2 == t) live2 = live2 && act[t];
+    const int ooff = live2 ? (rs2 == 0 ? bs[0] : bs[NS - 1]) * D + (h0 + row - rs2 * G) * 64 : -1;
+    attn_normalize(st, [&](int r, int8_t v) {
+        const int o = __builtin_amdgcn_readlane(ooff, r);
+        if (o >= 0) a.out[o + lane] = v;
+    });
 }
 
 void launch_attn_decode(const AttnArgs& a, int S, int p, hipStream_t s) {
