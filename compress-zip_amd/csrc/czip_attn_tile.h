@@ -420,14 +420,16 @@ __device__ __forceinline__ double bcast_f64(double x, int lane) {
 }
 
 // Normalization (attention.rs:278-285): emit(r, clamp127(div_rne(vacc[r], S_r)))
-// for the 16 rows, lane = head dim, S = 0 read as 1 (div_rne of
-// primitives.rs:163-185: the quotient of |v| rounded half to even, then the
-// sign).  In f64 from one reciprocal per row (lanes = rows): q = rint(min(|v|
-// * (1/S), 128)) is the rounded quotient unless it is a tie, the estimate
-// being within 128.5 * 2^-52 of |v| / S while a quotient that is no tie lies
-// at least 1/(2S) >= 2^-33 from every half-integer; r2 = 2 (|v| - q S) is
-// exact (q S < 2^40) and equals +-S exactly at a tie, where the even
-// neighbour wins.  Quotients from 127.5 up give 127 (the clamp).
+// for the 16 rows, lane = head dim, S = 0 read as 1.  div_rne
+// (primitives.rs:163-185) rounds the magnitude of the quotient half to even
+// and restores the sign, which is round-half-even of the signed quotient.  In f64 from
+// one reciprocal per row (lanes = rows): q = rint(v * (1/S)) is within 2^-22
+// of v / S (|v / S| <= 2^31), so for |v / S| <= 2^8 it is the rounded quotient
+// unless that is a tie (a quotient that is no tie lies at least 1/(2S) >=
+// 2^-33 from every half-integer), and beyond that the clamp decides.  r2 =
+// 2 fma(-q, S, v) is exact (the remainder is an integer below 2^32 in
+// magnitude) and equals +-S exactly at a tie, where the even neighbour of q
+// in the direction of r2 wins: (q + (r2 > 0)) & ~1.
 template <class Emit>
 __device__ __forceinline__ void attn_normalize(const AttnRows& st, Emit emit) {
     const double dl = (double)max(st.S, 1u);
@@ -435,15 +437,12 @@ __device__ __forceinline__ void attn_normalize(const AttnRows& st, Emit emit) {
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const double inv = bcast_f64(il, r), den = bcast_f64(dl, r);
-        const int n = (int)st.vacc[r];
-        const unsigned an = n < 0 ? 0u - (unsigned)n : (unsigned)n;
-        const double af = (double)an;
-        const double q = __builtin_rint(__builtin_fmin(af * inv, 128.0));
-        const double r2 = 2.0 * __builtin_fma(-q, den, af);
-        unsigned qi = (unsigned)q;
-        const unsigned odd = __builtin_fabs(r2) == den ? (qi & 1u) : 0u;
-        qi = min(r2 > 0.0 ? qi + odd : qi - odd, 127u);
-        emit(r, (int8_t)(n < 0 ? -(int)qi : (int)qi));
+        const double nf = (double)(int)st.vacc[r];
+        const double q = __builtin_rint(nf * inv);
+        const double r2 = 2.0 * __builtin_fma(-q, den, nf);
+        const int qi = (int)q;
+        const int qt = __builtin_fabs(r2) == den ? (qi + (r2 > 0.0 ? 1 : 0)) & ~1 : qi;
+        emit(r, (int8_t)clamp127(qt));
     }
 }
 
