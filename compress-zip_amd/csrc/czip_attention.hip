@@ -64,6 +64,9 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void k_attention(AttnArgs a) {
 
     const int last = min(wrow0 + 15, len - 1);  // the wave's last visible key
     const int ntiles = last / 64 + 1;
+    // the last tile is a half tile (keys t0 .. t0 + 31) when the wave's
+    // visible keys end in its first half
+    const bool half_last = (last & 63) < 32;
     // K [T][64] and V^T [TP/16][64][16] of the chunk's KV head: buffer loads
     // with the tile offset in the scalar operand; keys past T read as 0 (the
     // resource's range check) and are never visible.
@@ -71,28 +74,49 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void k_attention(AttnArgs a) {
     const int8_t* Vg = a.vc + ((size_t)b * a.KH + g) * 64 * a.TP;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)Kg, (short)0, T * 64, BUF_DWORD3);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)Vg, (short)0, a.TP * 64, BUF_DWORD3);
-    const int kofs = (16 * (row >> 2) + (row & 3)) * 64 + grp * 16;  // key kperm(blk, row) = this + 4 blk rows
-    const int vofs = grp * 1024 + row * 16;                           // block grp of 16 keys, dim row (+ 16 db)
+    // key kperm<KT>(blk, row) = the row's base + 4 blk; V^T of dim row (+ 16
+    // db), keys 16 grp .. +16 of the tile
+    const int kofs = (16 * (row >> 2) + (row & 3)) * 64 + grp * 16;
+    const int vofs = grp * 1024 + row * 16;
     auto load_k = [&](int blk, int t0) { return __builtin_amdgcn_raw_buffer_load_b128(rk, kofs + blk * 256, t0 * 64, 0); };
     auto load_v = [&](int db, int t0) { return __builtin_amdgcn_raw_buffer_load_b128(rv, vofs + db * 256, t0 * 64, 0); };
     // one register set each: this tile's V^T is requested as the tile starts
     // (it arrives during the scores and the scan), the next tile's K once the
-    // passes are done (the last tile reloads itself, so the loads stay
+    // passes are done (the last full tile reloads itself, so the loads stay
     // unconditional)
+    const int nfull = half_last ? ntiles - 1 : ntiles;
     v4i kc[4], vc[4];
+    if (nfull > 0) {
 #pragma unroll
-    for (int blk = 0; blk < 4; blk++) kc[blk] = load_k(blk, 0);
-    for (int kt = 0; kt < ntiles; kt++) {
+        for (int blk = 0; blk < 4; blk++) kc[blk] = load_k(blk, 0);
+    }
+    for (int kt = 0; kt < nfull; kt++) {
         const int t0 = kt * 64;
-        const int tn = t0 + 64 <= last ? t0 + 64 : t0;
 #pragma unroll
         for (int db = 0; db < 4; db++) vc[db] = load_v(db, t0);
-        int nvalid = p - (t0 + grp * 16) + 1;  // keys t <= p are visible (causal)
-        nvalid = nvalid < 0 ? 0 : (nvalid > 16 ? 16 : nvalid);
-        attn_tile<GEN, 1>([&](int, int blk) { return kc[blk]; }, [&](int, int db) { return vc[db]; }, &qop, 0,
-                          mscale, nvalid, t0 + 63 > wrow0, etb, W, st);
+        const int nvalid = min(max(p - (t0 + grp * 16) + 1, 0), 16);  // keys t <= p are visible (causal)
+        attn_tile<GEN, 1, 64>([&](int, int blk) { return kc[blk]; }, [&](int, int db) { return vc[db]; }, &qop, 0,
+                              mscale, nvalid, t0 + 63 > wrow0, etb, W, st);
+        const int tn = kt + 1 < nfull ? t0 + 64 : t0;
 #pragma unroll
         for (int blk = 0; blk < 4; blk++) kc[blk] = load_k(blk, tn);
+    }
+    if (half_last) {
+        // keys t0 .. t0 + 31, requested here rather than in the loop (their
+        // offsets would stay live across it): K rows kperm<32>, V^T of keys
+        // 8 grp .. +8 (8 bytes of a 16-key block)
+        const int t0 = nfull * 64;
+        const int ko = (8 * (row >> 2) + (row & 3)) * 64 + grp * 16, vo = (grp >> 1) * 1024 + (grp & 1) * 8 + row * 16;
+#pragma unroll
+        for (int blk = 0; blk < 2; blk++) kc[blk] = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + blk * 256, t0 * 64, 0);
+#pragma unroll
+        for (int db = 0; db < 4; db++) {
+            const auto x = __builtin_amdgcn_raw_buffer_load_b64(rv, vo + db * 256, t0 * 64, 0);
+            vc[db] = (v4i){(int)x[0], (int)x[1], 0, 0};
+        }
+        const int nvalid = min(max(p - (t0 + grp * 8) + 1, 0), 8);
+        attn_tile<GEN, 1, 32>([&](int, int blk) { return kc[blk]; }, [&](int, int db) { return vc[db]; }, &qop, 0,
+                              mscale, nvalid, true, etb, W, st);
     }
 
     int8_t* const orow = a.out + ((size_t)b * T + wrow0) * D + h * 64;

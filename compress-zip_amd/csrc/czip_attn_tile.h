@@ -133,10 +133,13 @@ __device__ __forceinline__ unsigned spread_b7(unsigned z, unsigned sel) { return
 __device__ __forceinline__ unsigned pick(unsigned msk, unsigned a, unsigned b) { return (a & msk) | (b & ~msk); }
 
 // The K operand's row m of MFMA block blk holds key kperm(blk, m) of the tile,
-// so that the score block's output lane (row, g) receives keys 16 g + 4 blk
-// + (0..3): after the 4 blocks each lane holds 16 consecutive keys of its
-// row, the order of the scan, with no transpose.
-__device__ __forceinline__ int kperm(int blk, int m) { return 16 * (m >> 2) + 4 * blk + (m & 3); }
+// so that the score block's output lane (row, g) receives keys KT/4 g + 4 blk
+// + (0..3): after the KT/16 blocks each lane holds KT/4 consecutive keys of
+// its row, the order of the scan, with no transpose.  KT = 64 (a full tile) or
+// 32 (a half tile: the last tile of a row block whose visible keys end in its
+// first half).
+template <int KT = 64>
+__device__ __forceinline__ int kperm(int blk, int m) { return (KT / 4) * (m >> 2) + 4 * blk + (m & 3); }
 
 // Running state of a wave's 16 rows: max m (attn_m_empty / the scan's
 // representation) and weight sum S with lanes = rows (replicated over the 4
@@ -147,13 +150,16 @@ struct AttnRows {
     unsigned vacc[16];
 };
 
-// One 64-key tile.  kop(s, blk): the K operand of key kperm(blk, lane%16),
-// head dims 16*(lane/16) .. +16; vop(s, db): the V^T operand of head dim
-// 16*db + lane%16, keys 16*(lane/16) .. +16 (each called once per index,
-// the V operands after the scan).  etb: the exp table of attn_etab_host in LDS.
-// nvalid: keys [16*(lane/16), +nvalid) of the lane's row are visible (the
-// others get weight 0 and are never records), used when diag is set.  Every
-// row of the wave is combined into vacc; the caller reads only its own rows.
+// One tile of KT keys (64, or 32 for a half tile: KT/16 score blocks, KT/4
+// keys per lane and the PV products on the 16x16x32 MFMA).  kop(s, blk): the
+// K operand of key kperm<KT>(blk, lane%16), head dims 16*(lane/16) .. +16;
+// vop(s, db): the V^T operand of head dim 16*db + lane%16, keys
+// KT/4*(lane/16) .. +KT/4 (a half tile uses its low 8 bytes; each called once
+// per index, the V operands after the scan).  etb: the exp table of
+// attn_etab_host in LDS.  nvalid: keys [KT/4*(lane/16), +nvalid) of the
+// lane's row are visible (the others get weight 0 and are never records),
+// used when diag is set.  Every row of the wave is combined into vacc; the
+// caller reads only its own rows.
 //
 // NS > 1 packs NS independent key streams (decode: streams sharing nothing
 // but the shape) into the wave's rows (rs: the lane's row's stream, NS for
@@ -163,19 +169,53 @@ struct AttnRows {
 // reads stream s, else 0), the PV products with weight 0 in the other
 // streams' columns (a constant, corrected like the keys outside a segment).
 // NS == 1: qs[0] is the query operand and rs is unused.
-template <bool GEN, int NS, class KOp, class VOp>
+// the PV-side operand types and product of a tile of KT keys: 16 bytes of 16
+// keys per lane (16x16x64) or 8 bytes of 8 keys (16x16x32)
+template <int KT>
+struct AttnPv {
+    using Op = v4i;
+    static constexpr v4i ONES = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    static __device__ __forceinline__ Op op(v4i v) { return v; }
+    static __device__ __forceinline__ Op from_dw(const unsigned* d) {
+        return (v4i){(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+    }
+    static __device__ __forceinline__ v4i mma(Op a, Op b, v4i c) {
+        return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct AttnPv<32> {
+    using Op = long;
+    static constexpr long ONES = 0x0101010101010101l;
+    static __device__ __forceinline__ Op op(v4i v) {
+        return (long)(((unsigned long long)(unsigned)v[1] << 32) | (unsigned)v[0]);
+    }
+    static __device__ __forceinline__ Op from_dw(const unsigned* d) {
+        return (long)(((unsigned long long)d[1] << 32) | d[0]);
+    }
+    static __device__ __forceinline__ v4i mma(Op a, Op b, v4i c) {
+        return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+    }
+};
+
+template <bool GEN, int NS, int KT, class KOp, class VOp>
 __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, int rs, double mscale,
                                           int nvalid, bool diag, const uint16_t* etb, AttnWaveLds& W,
                                           AttnRows& st) {
+    static_assert(KT == 64 || KT == 32, "a tile holds 64 or 32 keys");
+    constexpr int KPL = KT / 4;   // keys per lane
+    constexpr int NDW = KPL / 4;  // dwords of weight bytes per lane = score blocks
+    using Pv = AttnPv<KT>;
+    using Op = typename Pv::Op;
     const int lane = threadIdx.x & 63, row = lane & 15, grp = lane >> 4;
 
     // 1. S^T = K Q^T and the score epilogue: lane (row, grp) gets the scores
-    // of keys 16*grp .. +16 of its row (kperm)
-    unsigned sv[16];
+    // of keys KPL*grp .. +KPL of its row (kperm)
+    unsigned sv[KPL];
     {
         const double ms4 = mscale * 0.25, cbu = score_bias_u(mscale);
 #pragma unroll
-        for (int blk = 0; blk < 4; blk++) {
+        for (int blk = 0; blk < NDW; blk++) {
             v4i sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(0, blk), qs[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
             for (int t = 1; t < NS; t++) sc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop(t, blk), qs[t], sc, 0, 0, 0);
@@ -185,10 +225,10 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
         }
     }
 
-    // 2. in-order scan of keys [16*grp, 16*grp+16) of this row
+    // 2. in-order scan of keys [KPL*grp, KPL*grp+KPL) of this row
     if (diag) {
 #pragma unroll
-        for (int k = 0; k < 16; k++)
+        for (int k = 0; k < KPL; k++)
             if (k >= nvalid) sv[k] = (unsigned)attn_m_empty<GEN>();  // never a record; weight masked below
     }
     // the running max entering this lane's keys: the row's max so far and the
@@ -196,7 +236,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
     auto vmax = [](unsigned a, unsigned b) { return GEN ? (unsigned)max((int)a, (int)b) : max(a, b); };
     unsigned bmax = sv[0];
 #pragma unroll
-    for (int k = 1; k < 16; k++) bmax = vmax(bmax, sv[k]);
+    for (int k = 1; k < KPL; k++) bmax = vmax(bmax, sv[k]);
     const unsigned e1 = (unsigned)__shfl((int)bmax, (lane - 16) & 63, 64),
                    e2 = (unsigned)__shfl((int)bmax, (lane - 32) & 63, 64),
                    e3 = (unsigned)__shfl((int)bmax, (lane - 48) & 63, 64);
@@ -205,14 +245,14 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
     if (grp >= 2) cur0 = vmax(cur0, e2);
     if (grp >= 3) cur0 = vmax(cur0, e3);
     // weights (offset bytes, WB) and rescale factors (^ WB): one exp per key,
-    // no branches, so the 16 table reads can be in flight together
-    unsigned xs[16], ws[16];  // rescale factor (or weight) of each key, and its weight (65535 at a record)
+    // no branches, so the table reads can be in flight together
+    unsigned xs[KPL], ws[KPL];  // rescale factor (or weight) of each key, and its weight (65535 at a record)
     unsigned recm = 0u;   // bit k: key k is a record
     unsigned fresh = 0u;  // bit k: key k is a record over "nothing seen": no rescale, no split
     if (GEN) {
         int M = (int)cur0;
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
+        for (int k = 0; k < KPL; k++) {
             const int s = (int)sv[k];
             const bool rec = s > M;
             const int d = (int)(rec ? (unsigned)M - (unsigned)s : (unsigned)s - (unsigned)M);  // i32 wrap, as the reference
@@ -224,15 +264,15 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
             M = max(M, s);
         }
     } else {
-        // three phases, so that the 16 table reads are in flight together:
+        // three phases, so that the table reads are in flight together:
         // the running max and every key's table step, the reads, the
         // weights.  Only the lane's first key can meet "nothing seen" as a
         // record (masked keys are a suffix).
-        unsigned tk[16];
-        bool recb[16];
+        unsigned tk[KPL];
+        bool recb[KPL];
         unsigned M = cur0;
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
+        for (int k = 0; k < KPL; k++) {
             const unsigned s = sv[k];
             recb[k] = s > M;
             tk[k] = exp_step_u(absdiff_u32(s, M));
@@ -241,12 +281,12 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
         }
         fresh = recb[0] && cur0 == 0u ? 1u : 0u;
         __builtin_amdgcn_sched_barrier(0);
-        unsigned eb[16];
+        unsigned eb[KPL];
 #pragma unroll
-        for (int k = 0; k < 16; k++) eb[k] = etb[tk[k]];
+        for (int k = 0; k < KPL; k++) eb[k] = etb[tk[k]];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
+        for (int k = 0; k < KPL; k++) {
             ws[k] = recb[k] ? 0x7F7Fu : eb[k];  // a record's weight E(0) = 65535
             xs[k] = eb[k];
         }
@@ -258,28 +298,39 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
     const unsigned splm = recm & ~fresh;
     const unsigned g0 = (unsigned)__shfl((int)splm, row, 64), g1 = (unsigned)__shfl((int)splm, row + 16, 64),
                    g2 = (unsigned)__shfl((int)splm, row + 32, 64), g3 = (unsigned)__shfl((int)splm, row + 48, 64);
-    unsigned rlo = g0 | (g1 << 16), rhi = g2 | (g3 << 16);
+    // the row's splits as a KT-bit mask (bit = key of the tile) in rlo:rhi
+    unsigned rlo, rhi, blo, bhi;
+    if constexpr (KT == 64) {
+        rlo = g0 | (g1 << 16);
+        rhi = g2 | (g3 << 16);
+        blo = grp == 0 ? 0u : (grp == 1 ? 0xFFFFu : 0xFFFFFFFFu);
+        bhi = grp == 3 ? 0xFFFFu : 0u;
+    } else {
+        rlo = g0 | (g1 << 8) | (g2 << 16) | (g3 << 24);
+        rhi = 0u;
+        blo = (1u << (8 * grp)) - 1u;
+        bhi = 0u;
+    }
     const int nrow = __builtin_popcount(rlo) + __builtin_popcount(rhi);
-    const unsigned blo = grp == 0 ? 0u : (grp == 1 ? 0xFFFFu : 0xFFFFFFFFu), bhi = grp == 3 ? 0xFFFFu : 0u;
     const unsigned seg = (unsigned)(__builtin_popcount(rlo & blo) + __builtin_popcount(rhi & bhi));
     // every key's factor, read at its split's pass
-    {
-        uint4 e0, e1v;
-        e0.x = __builtin_amdgcn_perm(xs[1], xs[0], 0x05040100u); e0.y = __builtin_amdgcn_perm(xs[3], xs[2], 0x05040100u);
-        e0.z = __builtin_amdgcn_perm(xs[5], xs[4], 0x05040100u); e0.w = __builtin_amdgcn_perm(xs[7], xs[6], 0x05040100u);
-        e1v.x = __builtin_amdgcn_perm(xs[9], xs[8], 0x05040100u); e1v.y = __builtin_amdgcn_perm(xs[11], xs[10], 0x05040100u);
-        e1v.z = __builtin_amdgcn_perm(xs[13], xs[12], 0x05040100u); e1v.w = __builtin_amdgcn_perm(xs[15], xs[14], 0x05040100u);
-        *(uint4*)&W.ex[row][grp * 16] = e0;
-        *(uint4*)&W.ex[row][grp * 16 + 8] = e1v;
+#pragma unroll
+    for (int h = 0; h < KPL / 8; h++) {
+        uint4 e;
+        e.x = __builtin_amdgcn_perm(xs[8 * h + 1], xs[8 * h], 0x05040100u);
+        e.y = __builtin_amdgcn_perm(xs[8 * h + 3], xs[8 * h + 2], 0x05040100u);
+        e.z = __builtin_amdgcn_perm(xs[8 * h + 5], xs[8 * h + 4], 0x05040100u);
+        e.w = __builtin_amdgcn_perm(xs[8 * h + 7], xs[8 * h + 6], 0x05040100u);
+        *(uint4*)&W.ex[row][grp * KPL + 8 * h] = e;
     }
     // weights as signed byte pairs (the bytes of w ^ WB) and segment bytes
     // dd = 128 + the key's segment id (splits up to and including the key,
-    // <= 64): byte k of a dword = key 16*grp + 4*i + k.  Pass j keeps
+    // <= 64): byte k of a dword = key KPL*grp + 4*i + k.  Pass j keeps
     // dd - j * 0x01010101, whose bytes never borrow (63 <= 128 + id - j <= 192),
     // so bit 7 of a byte tells id >= j.
-    unsigned hi_dw[4], lo_dw[4], dd[4];
+    unsigned hi_dw[NDW], lo_dw[NDW], dd[NDW];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < NDW; i++) {
         const unsigned* w4 = ws + i * 4;
         const unsigned p01 = __builtin_amdgcn_perm(w4[1], w4[0], 0x05010400u);
         const unsigned p23 = __builtin_amdgcn_perm(w4[3], w4[2], 0x05010400u);
@@ -292,7 +343,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
     }
     if (diag) {  // invisible keys: weight 0 (bytes 0x80), in no segment (id 127: bit 7 stays set)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < NDW; i++) {
             const int q = nvalid - 4 * i;
             const unsigned vm = q >= 4 ? 0xFFFFFFFFu : (q <= 0 ? 0u : ((1u << (8 * q)) - 1u));
             hi_dw[i] = pick(vm, hi_dw[i], 0x80808080u);
@@ -309,19 +360,18 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
     int nmax = nrow;
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
-    // A operand of the PV product, and the sum over the tile's 64 keys (of
+    // A operand of the PV product, and the sum over the tile's KT keys (of
     // every stream) of v at head dim = lane: rows of ones times V, whose
     // output lane l holds column l % 16, i.e. dim 16 db + l % 16
-    constexpr v4i ONES = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-    v4i vop[NS][4];
+    Op vop[NS][4];
     int vsum = 0;
 #pragma unroll
     for (int db = 0; db < 4; db++) {
         v4i cs = {0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < NS; t++) {
-            vop[t][db] = vop_at(t, db);
-            cs = __builtin_amdgcn_mfma_i32_16x16x64_i8(ONES, vop[t][db], cs, 0, 0, 0);
+            vop[t][db] = Pv::op(vop_at(t, db));
+            cs = Pv::mma(Pv::ONES, vop[t][db], cs);
         }
         vsum = grp == db ? cs[0] : vsum;
     }
@@ -334,29 +384,37 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
 #pragma unroll
     for (int t = 0; t < NS; t++) sel[t] = NS == 1 || rs == t ? SEL_B7 : SEL_ZERO;
     for (int j = 0; j <= nmax; j++) {
-        v4i bhs[NS], bls[NS];
+        Op bhs[NS], bls[NS];
+        {
+            unsigned bh[NS][NDW], bl[NS][NDW];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const unsigned dn = dd[i] - 0x01010101u;
-            const unsigned m = dd[i] & ~dn;  // bit 7 of a byte: id >= j and not id >= j + 1
-            dd[i] = dn;
+            for (int i = 0; i < NDW; i++) {
+                const unsigned dn = dd[i] - 0x01010101u;
+                const unsigned m = dd[i] & ~dn;  // bit 7 of a byte: id >= j and not id >= j + 1
+                dd[i] = dn;
+#pragma unroll
+                for (int t = 0; t < NS; t++) {
+                    const unsigned msk = spread_b7(m, sel[t]);
+                    bh[t][i] = pick(msk, hi_dw[i], 0x80808080u);
+                    bl[t][i] = pick(msk, lo_dw[i], 0x80808080u);
+                }
+            }
 #pragma unroll
             for (int t = 0; t < NS; t++) {
-                const unsigned msk = spread_b7(m, sel[t]);
-                bhs[t][i] = (int)pick(msk, hi_dw[i], 0x80808080u);
-                bls[t][i] = (int)pick(msk, lo_dw[i], 0x80808080u);
+                bhs[t] = Pv::from_dw(bh[t]);
+                bls[t] = Pv::from_dw(bl[t]);
             }
         }
-        // sum over the row's 64 keys of (w_j - 32896) (rows of ones times the
+        // sum over the row's KT keys of (w_j - 32896) (rows of ones times the
         // weight columns: output lane l holds column l % 16 = the lane's
-        // row), less the other streams' columns (64 keys of -32896 each)
+        // row), less the other streams' columns (KT keys of -32896 each)
         v4i sh = {0, 0, 0, 0}, sl = {0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < NS; t++) {
-            sh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ONES, bhs[t], sh, 0, 0, 0);
-            sl = __builtin_amdgcn_mfma_i32_16x16x64_i8(ONES, bls[t], sl, 0, 0, 0);
+            sh = Pv::mma(Pv::ONES, bhs[t], sh);
+            sl = Pv::mma(Pv::ONES, bls[t], sl);
         }
-        const int sw = sh[0] * 256 + sl[0] + (NS - 1) * 64 * (int)WOFF;
+        const int sw = sh[0] * 256 + sl[0] + (NS - 1) * KT * (int)WOFF;
         // rescale factor of this lane's row at record j (0: none), the lowest
         // record not yet passed; row r's is read by the combine from lane r
         unsigned erow = 0u;
@@ -368,7 +426,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
         }
         // 4a. S of this lane's row (lanes = rows): rescale at record j, then add segment j
         if (erow) st.S = rescale_s(st.S, erow);
-        st.S += (unsigned)sw + 64u * WOFF;
+        st.S += (unsigned)sw + (unsigned)KT * WOFF;
         // the high- and low-byte products of two head-dim blocks at a time are
         // independent, so their MFMAs issue back to back and one shift-add
         // joins them
@@ -377,12 +435,12 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
             v4i ah[2], al[2];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                ah[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[0][d2 + u], bhs[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
-                al[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[0][d2 + u], bls[0], (v4i){0, 0, 0, 0}, 0, 0, 0);
+                ah[u] = Pv::mma(vop[0][d2 + u], bhs[0], (v4i){0, 0, 0, 0});
+                al[u] = Pv::mma(vop[0][d2 + u], bls[0], (v4i){0, 0, 0, 0});
 #pragma unroll
                 for (int t = 1; t < NS; t++) {
-                    ah[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[t][d2 + u], bhs[t], ah[u], 0, 0, 0);
-                    al[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(vop[t][d2 + u], bls[t], al[u], 0, 0, 0);
+                    ah[u] = Pv::mma(vop[t][d2 + u], bhs[t], ah[u]);
+                    al[u] = Pv::mma(vop[t][d2 + u], bls[t], al[u]);
                 }
             }
 #pragma unroll

@@ -62,10 +62,11 @@ void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s) 
 // (16 bytes each) straight from the caches, one tile ahead: one stream into
 // a second register set, two streams in place (the next K and V after the
 // tile's passes; the V latency is covered by the scores and the scan, the K
-// latency by the other waves of the SIMD).
+// latency by the other waves of the SIMD).  Three waves per SIMD (168 VGPRs,
+// no scratch).
 // ---------------------------------------------------------------------------
 template <bool GEN, int NS>
-__global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a, int p, int G) {
+__global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int G) {
     __shared__ __attribute__((aligned(16))) uint16_t etb[ETB_PAD];
     __shared__ __attribute__((aligned(16))) AttnWaveLds wl[4];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -133,6 +134,9 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
     auto load_k = [&](int t, int blk, int t0) {
         return __builtin_amdgcn_raw_buffer_load_b128(rk[t], (t0 + kperm(blk, row)) * 64 + grp * 16, 0, 0);
     };
+    auto load_k_half = [&](int t, int blk, int t0) {
+        return __builtin_amdgcn_raw_buffer_load_b128(rk[t], (t0 + kperm<32>(blk, row)) * 64 + grp * 16, 0, 0);
+    };
     // V^T of the decode caches in 4-key blocks (vt_off, vl = 2): the operand's
     // 16 keys of one dim are four 4-byte words, 256 bytes apart
     auto load_v = [&](int t, int db, int t0) {
@@ -141,6 +145,12 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
                      (int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o + 256, 0, 0),
                      (int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o + 512, 0, 0),
                      (int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o + 768, 0, 0)};
+    };
+    // a half tile's operand: keys 8 grp .. +8 of one dim, two words
+    auto load_v_half = [&](int t, int db, int t0) {
+        const int o = vt_off(t0 + grp * 8, db * 16 + row, 2);
+        return (v4i){(int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o, 0, 0),
+                     (int)__builtin_amdgcn_raw_buffer_load_b32(rv[t], o + 256, 0, 0), 0, 0};
     };
     auto nvalid_at = [&](int t0) {
         const int n = p - (t0 + grp * 16) + 1;
@@ -152,7 +162,7 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
         // stay unconditional and nothing waits on them before their use
         auto tile = [&](v4i* kc, v4i* vc, v4i* kn, v4i* vn, int t0) {
             const int tn = t0 + 64 <= p ? t0 + 64 : t0;
-            attn_tile<GEN, 1>(
+            attn_tile<GEN, 1, 64>(
                 [&](int, int blk) {
                     kn[blk] = load_k(0, blk, tn);
                     return kc[blk];
@@ -174,34 +184,50 @@ __global__ __launch_bounds__(256, NS == 1 ? 3 : 2) void k_attn_decode(AttnArgs a
         }
         if (kt < ntiles) tile(k0, v0, k1, v1, kt * 64);
     } else {
-        // (all K loads before all V loads, as in the loop, so that the scores
-        // wait for the K operands only)
+        // the last tile is a half tile (keys t0 .. t0 + 31) when p falls in
+        // its first half.  Operands one tile ahead, all K loads before all V
+        // loads, so that the scores wait for the K operands only.
+        const bool half_last = (p & 63) < 32;
+        const int nfull = half_last ? ntiles - 1 : ntiles;
         v4i kr[NS][4], vr[NS][4];
+        auto load_full = [&](int t0) {
 #pragma unroll
-        for (int t = 0; t < NS; t++)
+            for (int t = 0; t < NS; t++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) kr[t][i] = load_k(t, i, 0);
-        __builtin_amdgcn_sched_barrier(0);
+                for (int i = 0; i < 4; i++) kr[t][i] = load_k(t, i, t0);
 #pragma unroll
-        for (int t = 0; t < NS; t++)
+            for (int t = 0; t < NS; t++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) vr[t][i] = load_v(t, i, 0);
-        for (int kt = 0; kt < ntiles; kt++) {
+                for (int i = 0; i < 4; i++) vr[t][i] = load_v(t, i, t0);
+        };
+        if (nfull > 0) load_full(0);
+        for (int kt = 0; kt < nfull; kt++) {
             const int t0 = kt * 64;
-            const int tn = t0 + 64 <= p ? t0 + 64 : t0;
-            attn_tile<GEN, NS>([&](int t, int blk) { return kr[t][blk]; }, [&](int t, int db) { return vr[t][db]; },
-                               qs, rs, mscale, nvalid_at(t0), t0 + 63 > p, etb, wl[wave], st);
+            attn_tile<GEN, NS, 64>([&](int t, int blk) { return kr[t][blk]; },
+                                   [&](int t, int db) { return vr[t][db]; }, qs, rs, mscale, nvalid_at(t0),
+                                   t0 + 63 > p, etb, wl[wave], st);
             // the next tile's K and V once the passes are done: no operand
             // register is live across the passes (168 VGPRs, three waves per
-            // SIMD; the next K requested after the scan held 210, two waves)
+            // SIMD; the next K requested after the scan held 210, two waves).
+            // The last full tile reloads itself (unconditional loads).
+            load_full(kt + 1 < nfull ? t0 + 64 : t0);
+        }
+        if (half_last) {
+            // requested here, not in the loop: their offsets would stay live
+            // across it; the latency is covered by the other waves, like a K
+            const int t0 = nfull * 64;
 #pragma unroll
             for (int t = 0; t < NS; t++)
 #pragma unroll
-                for (int blk = 0; blk < 4; blk++) kr[t][blk] = load_k(t, blk, tn);
+                for (int i = 0; i < 2; i++) kr[t][i] = load_k_half(t, i, t0);
 #pragma unroll
             for (int t = 0; t < NS; t++)
 #pragma unroll
-                for (int db = 0; db < 4; db++) vr[t][db] = load_v(t, db, tn);
+                for (int i = 0; i < 4; i++) vr[t][i] = load_v_half(t, i, t0);
+            const int nv = min(max(p - (t0 + grp * 8) + 1, 0), 8);
+            attn_tile<GEN, NS, 32>([&](int t, int blk) { return kr[t][blk]; },
+                                   [&](int t, int db) { return vr[t][db]; }, qs, rs, mscale, nv, true, etb,
+                                   wl[wave], st);
         }
     }
     // each lane forms the output offset of its row (-1: no live row), read
