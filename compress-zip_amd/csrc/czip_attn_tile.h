@@ -158,8 +158,9 @@ struct AttnRows {
 // per index, the V operands after the scan).  etb: the exp table of
 // attn_etab_host in LDS.  nvalid: keys [KT/4*(lane/16), +nvalid) of the
 // lane's row are visible (the others get weight 0 and are never records),
-// used when diag is set.  Every row of the wave is combined into vacc; the
-// caller reads only its own rows.
+// used when diag is set.  The first NR rows of the wave are combined into
+// vacc (the caller's rows among them; rows from NR on must stay without
+// records, as the rows of no stream are); the caller reads only its own.
 //
 // NS > 1 packs NS independent key streams (decode: streams sharing nothing
 // but the shape) into the wave's rows (rs: the lane's row's stream, NS for
@@ -198,11 +199,12 @@ struct AttnPv<32> {
     }
 };
 
-template <bool GEN, int NS, int KT, class KOp, class VOp>
+template <bool GEN, int NS, int KT, int NR = 16, class KOp, class VOp>
 __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, int rs, double mscale,
                                           int nvalid, bool diag, const uint16_t* etb, AttnWaveLds& W,
                                           AttnRows& st) {
     static_assert(KT == 64 || KT == 32, "a tile holds 64 or 32 keys");
+    static_assert(NR >= 1 && NR <= 16, "rows in use: the first NR of 16");
     constexpr int KPL = KT / 4;   // keys per lane
     constexpr int NDW = KPL / 4;  // dwords of weight bytes per lane = score blocks
     using Pv = AttnPv<KT>;
@@ -455,17 +457,17 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
         // 4b. vacc (lanes = head dims).  Every row adds: a row without a
         // segment j has w = 0 (bytes -128) in every column, so its product is
         // exactly -corr and it adds 0.
-        unsigned bv[16];
+        unsigned bv[NR];
 #pragma unroll
-        for (int r = 0; r < 16; r++) bv[r] = W.buf[r][lane];
+        for (int r = 0; r < NR; r++) bv[r] = W.buf[r][lane];
         if (resc) {
 #pragma unroll
-            for (int r = 0; r < 16; r++)
+            for (int r = 0; r < NR; r++)
                 if ((resc >> r) & 1ull)
                     st.vacc[r] = rescale_v(st.vacc[r], (unsigned)__builtin_amdgcn_readlane((int)erow, r));
         }
 #pragma unroll
-        for (int r = 0; r < 16; r++) st.vacc[r] += bv[r] + corr;
+        for (int r = 0; r < NR; r++) st.vacc[r] += bv[r] + corr;
         wave_lds_fence();
     }
 }
@@ -488,12 +490,12 @@ __device__ __forceinline__ double bcast_f64(double x, int lane) {
 // 2 fma(-q, S, v) is exact (the remainder is an integer below 2^32 in
 // magnitude) and equals +-S exactly at a tie, where the even neighbour of q
 // in the direction of r2 wins: (q + (r2 > 0)) & ~1.
-template <class Emit>
+template <int NR = 16, class Emit>
 __device__ __forceinline__ void attn_normalize(const AttnRows& st, Emit emit) {
     const double dl = (double)max(st.S, 1u);
     const double il = 1.0 / dl;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
+    for (int r = 0; r < NR; r++) {
         const double inv = bcast_f64(il, r), den = bcast_f64(dl, r);
         const double nf = (double)(int)st.vacc[r];
         const double q = __builtin_rint(nf * inv);

@@ -65,7 +65,7 @@ void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s) 
 // latency by the other waves of the SIMD).  Three waves per SIMD (168 VGPRs,
 // no scratch).
 // ---------------------------------------------------------------------------
-template <bool GEN, int NS>
+template <bool GEN, int NS, int NR>
 __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int G) {
     __shared__ __attribute__((aligned(16))) uint16_t etb[ETB_PAD];
     __shared__ __attribute__((aligned(16))) AttnWaveLds wl[4];
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int G
         if (nfull > 0) load_full(0);
         for (int kt = 0; kt < nfull; kt++) {
             const int t0 = kt * 64;
-            attn_tile<GEN, NS, 64>([&](int t, int blk) { return kr[t][blk]; },
+            attn_tile<GEN, NS, 64, NR>([&](int t, int blk) { return kr[t][blk]; },
                                    [&](int t, int db) { return vr[t][db]; }, qs, rs, mscale, nvalid_at(t0),
                                    t0 + 63 > p, etb, wl[wave], st);
             // the next tile's K and V once the passes are done: no operand
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int G
 #pragma unroll
                 for (int i = 0; i < 4; i++) vr[t][i] = load_v_half(t, i, t0);
             const int nv = min(max(p - (t0 + grp * 8) + 1, 0), 8);
-            attn_tile<GEN, NS, 32>([&](int t, int blk) { return kr[t][blk]; },
+            attn_tile<GEN, NS, 32, NR>([&](int t, int blk) { return kr[t][blk]; },
                                    [&](int t, int db) { return vr[t][db]; }, qs, rs, mscale, nv, true, etb,
                                    wl[wave], st);
         }
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int G
     for (int t = 0; t < NS; t++)
         if (rs2 == t) live2 = live2 && act[t];
     const int ooff = live2 ? (rs2 == 0 ? bs[0] : bs[NS - 1]) * D + (h0 + row - rs2 * G) * 64 : -1;
-    attn_normalize(st, [&](int r, int8_t v) {
+    attn_normalize<NR>(st, [&](int r, int8_t v) {
         const int o = __builtin_amdgcn_readlane(ooff, r);
         if (o >= 0) a.out[o + lane] = v;
     });
@@ -253,13 +253,23 @@ void launch_attn_decode(const AttnArgs& a, int S, int p, hipStream_t s) {
     const bool two = 2 * G <= 16;
     const long long waves = (long long)(two ? (S + 1) / 2 : S) * a.KH;
     dim3 grid((unsigned)((waves + 3) / 4));
-    if (two) {
-        if (a.general) hipLaunchKernelGGL((k_attn_decode<true, 2>), grid, dim3(256), 0, s, g, p, G);
-        else hipLaunchKernelGGL((k_attn_decode<false, 2>), grid, dim3(256), 0, s, g, p, G);
+    // rows in use per wave (NS G of 16), rounded up to 8, 12 or 16
+    const int nr = !two ? 16 : (2 * G <= 8 ? 8 : (2 * G <= 12 ? 12 : 16));
+#define CZIP_ATTN_DEC(GEN, NS, NR) hipLaunchKernelGGL((k_attn_decode<GEN, NS, NR>), grid, dim3(256), 0, s, g, p, G)
+    if (!two) {
+        if (a.general) CZIP_ATTN_DEC(true, 1, 16);
+        else CZIP_ATTN_DEC(false, 1, 16);
+    } else if (nr == 8) {
+        if (a.general) CZIP_ATTN_DEC(true, 2, 8);
+        else CZIP_ATTN_DEC(false, 2, 8);
+    } else if (nr == 12) {
+        if (a.general) CZIP_ATTN_DEC(true, 2, 12);
+        else CZIP_ATTN_DEC(false, 2, 12);
     } else {
-        if (a.general) hipLaunchKernelGGL((k_attn_decode<true, 1>), grid, dim3(256), 0, s, g, p, G);
-        else hipLaunchKernelGGL((k_attn_decode<false, 1>), grid, dim3(256), 0, s, g, p, G);
+        if (a.general) CZIP_ATTN_DEC(true, 2, 16);
+        else CZIP_ATTN_DEC(false, 2, 16);
     }
+#undef CZIP_ATTN_DEC
 }
 
 // ---------------------------------------------------------------------------
