@@ -109,6 +109,50 @@ __device__ __forceinline__ void rowblock_mma(const int8_t* A, int M, int K, cons
     if (kt < nk) step(kt, w0, w1);
 }
 
+// The same product with the row block's whole A (64 rows x K) staged in LDS
+// at once (As: K / 64 tiles of [64][64], 64-byte permuted rows), one barrier,
+// then the K steps without barriers, each wave's W one step ahead.  The
+// workgroup's threads (any multiple of 64) share the staging.
+template <int CT>
+__device__ __forceinline__ void rowblock_mma_full(const int8_t* A, int M, int K, const int8_t* Wf, int wrows, int m0,
+                                                  int nb, int8_t (*As)[64 * 64], v4i (&acc)[4][CT]) {
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15;
+    const int nkt = K / 64;
+    const int arows = M - m0 < 64 ? M - m0 : 64;
+    const __amdgpu_buffer_rsrc_t rA =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(A + (size_t)m0 * K), (short)0, arows * K, BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)Wf, (short)0, wrows * K, BUF_DWORD3);
+    const int woff = (nb >> 4) * nkt * 1024 + lane * 16;
+    v4i w0[CT], w1[CT];
+    auto fetch_w = [&](v4i* w, int kt) {
+#pragma unroll
+        for (int t = 0; t < CT; t++) w[t] = __builtin_amdgcn_raw_buffer_load_b128(rW, woff + t * nkt * 1024, kt * 1024, 0);
+    };
+    fetch_w(w0, 0);
+    // chunk c: K step c / 256, row (c / 4) % 64, 16-byte piece c % 4
+    for (int c = tid; c < nkt * 256; c += (int)blockDim.x) {
+        const v4i x = __builtin_amdgcn_raw_buffer_load_b128(rA, ((c >> 2) & 63) * K + (c >> 8) * 64 + (c & 3) * 16, 0, 0);
+        *(v4i*)(As[c >> 8] + lds64((c >> 2) & 63, c & 3)) = x;
+    }
+    __syncthreads();
+    auto step = [&](int kt, const v4i* wc, v4i* wn) {
+        if (kt + 1 < nkt) fetch_w(wn, kt + 1);
+        v4i af[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[kt] + lds64(i * 16 + lr, lane >> 4));
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int t = 0; t < CT; t++) acc[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wc[t], af[i], acc[i][t], 0, 0, 0);
+    };
+    int kt = 0;
+    for (; kt + 1 < nkt; kt += 2) {
+        step(kt, w0, w1);
+        step(kt + 1, w1, w0);
+    }
+    if (kt < nkt) step(kt, w0, w1);
+}
+
 // rint(a * b) (round half to even) for |a * b| < 2^31, exact when a * b is
 // exact in f64: adding 1.5 * 2^52 makes the ulp 1, so the FMA's single
 // rounding lands on the integer, and the low word of the sum is that integer

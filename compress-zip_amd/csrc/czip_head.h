@@ -20,8 +20,9 @@ constexpr int HBM_ROWS = 64, HNW = 16;
 // whatever lut[0] holds).
 constexpr int ETAB_N = 4098;
 
+constexpr int HEAD_KMAX = 1024;  // the whole K of a row block staged at once (d_model <= 1024)
 struct HeadLds {
-    int8_t As[2][HBM_ROWS * 64] __attribute__((aligned(16)));
+    int8_t As[HEAD_KMAX / 64][HBM_ROWS * 64] __attribute__((aligned(16)));
     unsigned etab[ETAB_N + 2];
     int red_a[HNW][HBM_ROWS];
     unsigned red_b[HNW][HBM_ROWS], red_c[HNW][HBM_ROWS];
@@ -30,7 +31,7 @@ struct HeadLds {
     double row_y[HBM_ROWS];
 };
 
-// Logits of the block (rowblock_mma), then per row, with two block reductions:
+// Logits of the block (rowblock_mma_full), then per row, with two block reductions:
 //   1. max logit;
 //   2. first argmax (row_am) and S = sum E(l - max) (softmax_cdf.rs:96-110,
 //      coef < 2^24);
@@ -57,7 +58,7 @@ __device__ __forceinline__ void head_freqs(const int8_t* A, int M, int K, const 
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int t = 0; t < CT; t++) acc[i][t] = (v4i){0, 0, 0, 0};
-    rowblock_mma<CT>(A, M, K, W, V, m0, nb, L.As, acc);
+    rowblock_mma_full<CT>(A, M, K, W, V, m0, nb, L.As, acc);
 
     // 1. row max
 #pragma unroll
