@@ -700,9 +700,10 @@ __device__ __forceinline__ void rn_epilogue(const RowGemmArgs& a, v4i (&acc)[4][
     }
 }
 
-template <int NW, int CT, bool FAST>
+template <int NW, int CT, bool FAST, bool FULL>
 __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
-    __shared__ __attribute__((aligned(16))) int8_t As[2][RBM * 64];
+    // FULL: the block's whole A (K <= 1024) staged at once, K steps without barriers
+    __shared__ __attribute__((aligned(16))) int8_t As[FULL ? 16 : 2][RBM * 64];
     __shared__ unsigned red[NW][RBM];
     __shared__ int inv_s[RBM];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -716,7 +717,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn(RowGemmArgs a) {
 #pragma unroll
         for (int t = 0; t < CT; t++) acc[i][t] = (v4i){0, 0, 0, 0};
 
-    rowblock_mma<CT>(a.A, a.M, a.K, a.Wf, a.d, m0, nb, As, acc);
+    if constexpr (FULL) rowblock_mma_full<CT>(a.A, a.M, a.K, a.Wf, a.d, m0, nb, As, acc);
+    else rowblock_mma<CT>(a.A, a.M, a.K, a.Wf, a.d, m0, nb, As, acc);
     unsigned w1r[CT], w2r[CT];
 #pragma unroll
     for (int t = 0; t < CT; t++) {
@@ -885,10 +887,14 @@ template <int NW, int CT>
 static void launch_rn(const RowGemmArgs& a, hipStream_t s) {
     if (try_rn_splitk<NW, CT>(a, s)) return;
     dim3 grid((unsigned)((a.M + RBM - 1) / RBM));
-    if (a.rq_fast)
-        hipLaunchKernelGGL((k_gemm_rn<NW, CT, true>), grid, dim3(64 * NW), 0, s, a);
-    else
-        hipLaunchKernelGGL((k_gemm_rn<NW, CT, false>), grid, dim3(64 * NW), 0, s, a);
+    const bool full = a.K <= 1024;
+    if (a.rq_fast) {
+        if (full) hipLaunchKernelGGL((k_gemm_rn<NW, CT, true, true>), grid, dim3(64 * NW), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_rn<NW, CT, true, false>), grid, dim3(64 * NW), 0, s, a);
+    } else {
+        if (full) hipLaunchKernelGGL((k_gemm_rn<NW, CT, false, true>), grid, dim3(64 * NW), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_rn<NW, CT, false, false>), grid, dim3(64 * NW), 0, s, a);
+    }
 }
 
 // d = 64 h columns over NW waves of CT 16-wide tiles: 8 waves where h is even
