@@ -131,7 +131,7 @@ struct czip_job {
     uint8_t* d_data = nullptr;
     int64_t *d_offs = nullptr, *d_toff = nullptr, *st_bpos = nullptr;
     int32_t *d_blen = nullptr, *d_ntok = nullptr, *st_bit = nullptr;
-    uint32_t *d_tokens = nullptr, *st_low = nullptr, *st_high = nullptr, *st_code = nullptr;
+    uint32_t *d_tokens = nullptr, *st_low = nullptr, *st_high = nullptr, *st_code = nullptr, *st_plo = nullptr, *st_phi = nullptr;
     // step-wise decode session
     uint32_t *d_val = nullptr, *d_out = nullptr;
     std::vector<int32_t> h_lens;
@@ -929,11 +929,12 @@ extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t* data, co
     czip_status rc = CZIP_OK;
     auto& A = j->allocs;
     const size_t nc = (size_t)std::max(nchunks, 1);
-    if ((rc = dalloc(c, A, &j->d_data, (size_t)std::max<int64_t>(total_bytes, 1))) ||
+    if ((rc = dalloc(c, A, &j->d_data, (size_t)std::max<int64_t>(total_bytes, 1) + 16)) ||  // the decoder's word reads
         (rc = dalloc(c, A, &j->d_offs, nc)) || (rc = dalloc(c, A, &j->d_blen, nc)) ||
         (rc = dalloc(c, A, &j->d_ntok, nc)) || (rc = dalloc(c, A, &j->d_toff, nc)) ||
         (rc = dalloc(c, A, &j->d_tokens, (size_t)std::max<int64_t>(total_tokens, 1))) ||
         (rc = dalloc(c, A, &j->st_low, (size_t)S)) || (rc = dalloc(c, A, &j->st_high, (size_t)S)) ||
+        (rc = dalloc(c, A, &j->st_plo, (size_t)S)) || (rc = dalloc(c, A, &j->st_phi, (size_t)S)) ||
         (rc = dalloc(c, A, &j->st_code, (size_t)S)) || (rc = dalloc(c, A, &j->st_bpos, (size_t)S)) ||
         (rc = dalloc(c, A, &j->st_bit, (size_t)S)) || (rc = dalloc(c, A, &j->inp, (size_t)S)) ||
         (rc = dalloc(c, A, &j->x, (size_t)S * d)) || (rc = dalloc(c, A, &j->xn, (size_t)S * d)) ||
@@ -974,11 +975,14 @@ static czip_status run_decompress(czip_job* j) {
         const int S = (int)std::min<int64_t>(j->S, j->nchunks - g0);
         int steps = 0;
         for (int i = 0; i < S; i++) steps = std::max(steps, j->h_ntok[(size_t)(g0 + i)]);
-        DecState st{j->st_low, j->st_high, j->st_code, j->st_bpos, j->st_bit};
+        DecState st{j->st_low, j->st_high, j->st_code, j->st_bpos, j->st_bit, j->st_plo, j->st_phi};
         DecStreams ds{j->d_data, j->d_offs + g0, j->d_blen + g0, j->d_ntok + g0, j->d_tokens, j->d_toff + g0};
         { Timed t(c, "dec_init"); launch_dec_init(st, ds, S, s); }
         for (int p = 0; p < steps; p++) {
-            { Timed t(c, "dec_prep"); launch_dec_prep(ds, S, p, j->inp, s); }
+            {
+                Timed t(c, "dec_prep");
+                launch_dec_prep(ds, st, S, p, c->head_fused && p > 0, c->cfg.target_total, j->inp, s);
+            }
             if (!c->rn_fused) { Timed t(c, "embed_norm"); launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, S, d, j->x, j->xn, s); }
             for (int l = 0; l < c->cfg.n_layers; l++) {
                 const DevLayer& L = c->layers[(size_t)l];

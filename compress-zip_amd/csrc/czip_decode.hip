@@ -39,17 +39,76 @@ void launch_dec_init(DecState st, DecStreams ds, int S, hipStream_t s) {
     hipLaunchKernelGGL(k_dec_init, dim3((unsigned)((S + 63) / 64)), dim3(64), 0, s, st, ds, S);
 }
 
-// forward input of step p (main.rs:386-388)
-__global__ void k_dec_prep(DecStreams ds, int S, int p, uint32_t* __restrict__ inp) {
+// The decoder step of a decoded symbol with interval [lo, hi) (arith_coder.rs:243-262):
+// narrow (low, high), then renormalize, reading the stream's bits from an
+// 8-byte window: a step shifts at most 32 bits (each pass shifts a 0 into low
+// and a 1 into high; after 32 of them low = 0, high = 2^32 - 1 ends the loop).
+// The window comes from three aligned words of the chunk buffer (which carries
+// 16 bytes of padding); bytes at or past the chunk's end read as 0
+// (arith_coder.rs:176-190).
+__device__ __forceinline__ void dec_advance(DecState st, DecStreams ds, int b, unsigned lo, unsigned hi, unsigned total) {
+    const unsigned low = st.low[b], high = st.high[b], code = st.code[b];
+    const unsigned long long range = (unsigned long long)high - low + 1;
+    const double invT = 1.0 / (double)total;
+    unsigned long long nh = low + udiv64_32((unsigned long long)hi * range, total, invT) - 1;
+    unsigned long long nl = low + udiv64_32((unsigned long long)lo * range, total, invT);
+    unsigned long long cd = code;
+    const long long len = ds.blen[b];
+    const long long bp = st.byte_pos[b];
+    const int bi = st.bit_pos[b];
+    const long long start = ds.offs[b] + bp, base = start & ~3ll;
+    const unsigned* w = (const unsigned*)(ds.data + base);
+    const unsigned w0 = w[0], w1 = w[1], w2 = w[2];
+    const int sh = (int)(start - base) * 8;
+    const unsigned long long lo64 = ((unsigned long long)w1 << 32) | w0;
+    unsigned long long v = sh ? (lo64 >> sh) | ((unsigned long long)w2 << (64 - sh)) : lo64;  // bytes bp .. bp + 7
+    const long long nv = len - bp;
+    if (nv < 8) v = nv <= 0 ? 0ull : v & ((1ull << (8 * nv)) - 1ull);
+    const unsigned long long win = __builtin_bswap64(v);  // MSB first
+    int pos = 56 + bi;  // window bit of the next stream bit
+    for (;;) {
+        if (((nl ^ nh) & DHALF) == 0) {
+            nl = (nl << 1) & DMASK;
+            nh = ((nh << 1) & DMASK) | 1;
+            cd = ((cd << 1) & DMASK) | ((win >> pos) & 1);
+            pos--;
+        } else if ((nl & ~nh & DQUART) != 0) {
+            nl = ((nl << 1) ^ DHALF) & DMASK;
+            nh = (((nh ^ DHALF) << 1) | DHALF | 1) & DMASK;
+            cd = (cd & DHALF) | ((cd << 1) & (DMASK >> 1)) | ((win >> pos) & 1);
+            pos--;
+        } else {
+            break;
+        }
+    }
+    // reader position after the bits taken (it stops at the end of the chunk)
+    const long long used = (long long)(7 - bi) + (56 + bi - pos);
+    long long nbp = bp + used / 8;
+    int nbi = 7 - (int)(used % 8);
+    if (bp >= len) { nbp = bp; nbi = bi; }
+    else if (nbp >= len) { nbp = len; nbi = 7; }
+    st.low[b] = (uint32_t)nl;
+    st.high[b] = (uint32_t)nh;
+    st.code[b] = (uint32_t)cd;
+    st.byte_pos[b] = nbp;
+    st.bit_pos[b] = nbi;
+}
+
+// forward input of step p (main.rs:386-388), after the decoder step of step
+// p - 1's symbol when the fused head left it pending (upd)
+__global__ void k_dec_prep(DecStreams ds, DecState st, int S, int p, int upd, unsigned total, uint32_t* __restrict__ inp) {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= S) return;
+    const int n = ds.ntok[b];
+    if (upd && p <= n) dec_advance(st, ds, b, st.pend_lo[b], st.pend_hi[b], total);
     uint32_t t = 0u;
-    if (p < ds.ntok[b]) t = p == 0 ? BOS_TOKEN : ds.tokens[ds.tok_offs[b] + p - 1];
+    if (p < n) t = p == 0 ? BOS_TOKEN : ds.tokens[ds.tok_offs[b] + p - 1];
     inp[b] = t;
 }
 
-void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s) {
-    hipLaunchKernelGGL(k_dec_prep, dim3((unsigned)((S + 255) / 256)), dim3(256), 0, s, ds, S, p, inp);
+void launch_dec_prep(DecStreams ds, DecState st, int S, int p, bool upd, unsigned total, uint32_t* inp, hipStream_t s) {
+    hipLaunchKernelGGL(k_dec_prep, dim3((unsigned)((S + 255) / 256)), dim3(256), 0, s, ds, st, S, p, upd ? 1 : 0, total,
+                       inp);
 }
 
 // ---------------------------------------------------------------------------
@@ -553,47 +612,12 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
     }
     __syncthreads();
     if (!live) return;
-    const unsigned long long range = (unsigned long long)high - low + 1;
-    const double invT = 1.0 / (double)a.total;
-    unsigned long long nh = low + udiv64_32((unsigned long long)row_hi[lane] * range, a.total, invT) - 1;
-    unsigned long long nl = low + udiv64_32((unsigned long long)row_lo[lane] * range, a.total, invT);
-    unsigned long long cd = code;
-    // bits MSB first from byte bp, bit bi on (zeros past the end: arith_coder.rs:176-190)
-    const uint8_t* data = ds.data + ds.offs[b];
-    const long long len = ds.blen[b];
-    const long long bp = st.byte_pos[b];
-    const int bi = st.bit_pos[b];
-    unsigned long long win = 0;
-#pragma unroll
-    for (int k = 0; k < 8; k++) win |= (unsigned long long)(bp + k < len ? data[bp + k] : 0) << (56 - 8 * k);
-    int pos = 56 + bi;  // window bit of the next stream bit
-    for (;;) {
-        if (((nl ^ nh) & DHALF) == 0) {
-            nl = (nl << 1) & DMASK;
-            nh = ((nh << 1) & DMASK) | 1;
-            cd = ((cd << 1) & DMASK) | ((win >> pos) & 1);
-            pos--;
-        } else if ((nl & ~nh & DQUART) != 0) {
-            nl = ((nl << 1) ^ DHALF) & DMASK;
-            nh = (((nh ^ DHALF) << 1) | DHALF | 1) & DMASK;
-            cd = (cd & DHALF) | ((cd << 1) & (DMASK >> 1)) | ((win >> pos) & 1);
-            pos--;
-        } else {
-            break;
-        }
-    }
-    // reader position after the bits taken (it stops at the end of the chunk)
-    const long long used = (long long)(7 - bi) + (56 + bi - pos);
-    long long nbp = bp + used / 8;
-    int nbi = 7 - (int)(used % 8);
-    if (bp >= len) { nbp = bp; nbi = bi; }
-    else if (nbp >= len) { nbp = len; nbi = 7; }
-    st.low[b] = (uint32_t)nl;
-    st.high[b] = (uint32_t)nh;
-    st.code[b] = (uint32_t)cd;
-    st.byte_pos[b] = nbp;
-    st.bit_pos[b] = nbi;
+    // the symbol, and its interval for the decoder step, which the next
+    // step's input kernel applies (the workgroup ends here instead of
+    // waiting on one wave's bit reads)
     ds.tokens[ds.tok_offs[b] + a.p] = (uint32_t)row_sym[lane];
+    st.pend_lo[b] = row_lo[lane];
+    st.pend_hi[b] = row_hi[lane];
 }
 
 void launch_head_dec(const HeadDecArgs& a, DecState st, DecStreams ds, hipStream_t s) {

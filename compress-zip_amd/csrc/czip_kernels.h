@@ -190,6 +190,8 @@ struct DecState {        // one arithmetic decoder per stream (arith_coder.rs:13
     uint32_t* code;
     int64_t* byte_pos;
     int32_t* bit_pos;
+    uint32_t* pend_lo = nullptr;  // the last decoded symbol's interval [lo, hi) (fused head),
+    uint32_t* pend_hi = nullptr;  // applied to the decoder by the next step's input kernel
 };
 struct DecStreams {      // per stream of the current group
     const uint8_t* data;      // all chunk bytes
@@ -200,8 +202,10 @@ struct DecStreams {      // per stream of the current group
     const int64_t* tok_offs;  // [S] output offset of the stream's tokens
 };
 void launch_dec_init(DecState st, DecStreams ds, int S, hipStream_t s);
-// inputs of step p: BOS at p = 0, else the token decoded at p - 1; rows past ntok get 0
-void launch_dec_prep(DecStreams ds, int S, int p, uint32_t* inp, hipStream_t s);
+// inputs of step p: BOS at p = 0, else the token decoded at p - 1; rows past ntok get 0.
+// upd: first apply the pending decoder step of step p - 1's symbol (the fused head's
+// interval in st.pend_lo / pend_hi); total = the frequency total
+void launch_dec_prep(DecStreams ds, DecState st, int S, int p, bool upd, unsigned total, uint32_t* inp, hipStream_t s);
 // one query per (stream, head) at position p over cached keys 0..p
 void launch_attn_decode(const AttnArgs& a, int S, int p, hipStream_t s);
 // logits -> cumulative frequencies -> one arithmetic-decode step (arith_coder.rs:195-264)
