@@ -77,6 +77,8 @@ struct Stat {
 struct czip_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
+    hipStream_t lane_s[3] = {};  // a decode group's lanes after the first
+    hipEvent_t lane_ev[4] = {};  // fork / join of the lanes
     czip_model_desc cfg{};
     int KH = 1;  // cached KV heads per layer
     bool rn_fused = false;  // residual + norms fused into the row GEMM (gemm_rn_supported(d_model))
@@ -446,6 +448,8 @@ extern "C" void czip_destroy(czip_ctx* c) {
     for (auto& p : c->pending) { hipEventDestroy(p.a); hipEventDestroy(p.b); }
     for (auto e : c->event_pool) hipEventDestroy(e);
     for (void* p : c->allocs) hipFree(p);
+    for (auto e : c->lane_ev) if (e) hipEventDestroy(e);
+    for (auto q : c->lane_s) if (q) hipStreamDestroy(q);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;
 }
@@ -513,26 +517,43 @@ int pick_batch_chunks(const czip_ctx* c, int64_t nchunks, int T, bool logits = t
 // the final) normalized input in j->xn and the residual stream in j->x.  With
 // the row GEMM the projection outputs stay on chip; layer 0 re-reads its
 // residual input from the embedding rows of j->inp.
-void post_attention(czip_ctx* c, czip_job* j, int l, int M) {
+// A job's per-row buffers, or the rows of one decode lane (a contiguous range
+// of its streams) with its share of the split-K workspace
+struct RowBufs {
+    uint32_t* inp;
+    int16_t* x;
+    int8_t *xn, *q8, *attn, *y8, *r8;
+    int32_t* rn_ws;
+    size_t rn_ws_bytes;
+};
+
+RowBufs row_bufs(const czip_ctx* c, const czip_job* j, int64_t r0 = 0, int ws_parts = 1, int ws_part = 0) {
+    const size_t d = (size_t)c->cfg.d_model, F = (size_t)c->cfg.d_ff, r = (size_t)r0;
+    const size_t wb = j->rn_ws_bytes / (size_t)ws_parts / 16 * 16;
+    return RowBufs{j->inp + r, j->x + r * d, j->xn + r * d, j->q8 + r * d, j->attn + r * d,
+                   j->y8 ? j->y8 + r * d : nullptr, j->r8 ? j->r8 + r * F : nullptr,
+                   j->rn_ws ? j->rn_ws + wb / 4 * (size_t)ws_part : nullptr, wb};
+}
+
+void post_attention(czip_ctx* c, const RowBufs& r, int l, int M, hipStream_t s) {
     const int d = c->cfg.d_model, F = c->cfg.d_ff;
-    hipStream_t s = c->stream;
     const DevLayer& L = c->layers[(size_t)l];
     const bool last = l + 1 == c->cfg.n_layers;
     const int8_t* next = last ? c->final_norm : c->layers[(size_t)l + 1].attn_norm;
     if (c->rn_fused) {
         RowGemmArgs o{};
-        o.A = j->attn; o.W = L.out_w; o.Wf = L.out_wf; o.M = M; o.K = d; o.d = d;
+        o.A = r.attn; o.W = L.out_w; o.Wf = L.out_wf; o.M = M; o.K = d; o.d = d;
         set_requant(o, L.out_mult, L.out_shift);
         o.w1 = L.ffn_norm; o.w2 = L.post_attn_norm;
-        o.x_in = l == 0 ? nullptr : j->x; o.tok = j->inp; o.embed = c->embed;
-        o.x_out = j->x; o.xn = j->xn; o.ws = j->rn_ws; o.ws_bytes = j->rn_ws_bytes;
+        o.x_in = l == 0 ? nullptr : r.x; o.tok = r.inp; o.embed = c->embed;
+        o.x_out = r.x; o.xn = r.xn; o.ws = r.rn_ws; o.ws_bytes = r.rn_ws_bytes;
         { Timed t(c, "gemm_o_norm"); launch_gemm_rn(o, s); }
     } else {
         GemmArgs o{};
-        o.A = j->attn; o.W = L.out_w; o.M = M; o.N = d; o.K = d; o.out8 = j->y8; o.ldo = d;
+        o.A = r.attn; o.W = L.out_w; o.M = M; o.N = d; o.K = d; o.out8 = r.y8; o.ldo = d;
         set_requant(o, L.out_mult, L.out_shift);
         { Timed t(c, "gemm_o"); launch_gemm(o, EPI_REQ, s); }
-        { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.ffn_norm, L.post_attn_norm, M, d, j->xn, s); }
+        { Timed t(c, "row_norm"); launch_resid_norm(r.x, r.y8, L.ffn_norm, L.post_attn_norm, M, d, r.xn, s); }
     }
     // the fused FFN walks 128-row strips with one workgroup per CU: it pays
     // off for prefill sub-batches, while a decode step's few thousand rows
@@ -542,31 +563,31 @@ void post_attention(czip_ctx* c, czip_job* j, int l, int M) {
         u.K = d; set_requant(u, L.up_mult, L.up_shift);
         dn.K = F; set_requant(dn, L.down_mult, L.down_shift);
         FfnArgs f{};
-        f.xn = j->xn; f.Wup = L.up_wf16; f.Wdf = L.down_wf; f.M = M; f.d = d; f.F = F;
+        f.xn = r.xn; f.Wup = L.up_wf16; f.Wdf = L.down_wf; f.M = M; f.d = d; f.F = F;
         f.up_mult = u.mult; f.up_shift = u.shift; f.up_fast = u.rq_fast; f.up_scale = u.rq_scale;
         f.dn_mult = dn.mult; f.dn_shift = dn.shift; f.dn_fast = dn.rq_fast; f.dn_scale = dn.rq_scale;
-        f.w1 = L.post_ffn_norm; f.w2 = next; f.x_in = j->x; f.x_out = last ? nullptr : j->x; f.xn_out = j->xn;
+        f.w1 = L.post_ffn_norm; f.w2 = next; f.x_in = r.x; f.x_out = last ? nullptr : r.x; f.xn_out = r.xn;
         Timed t(c, "ffn");
         launch_ffn(f, s);
         return;
     }
     GemmArgs u{};
-    u.A = j->xn; u.W = L.up_w; u.M = M; u.N = 2 * F; u.K = d; u.out8 = j->r8; u.ldo = F;
+    u.A = r.xn; u.W = L.up_w; u.M = M; u.N = 2 * F; u.K = d; u.out8 = r.r8; u.ldo = F;
     set_requant(u, L.up_mult, L.up_shift);
     { Timed t(c, "gemm_up"); launch_gemm(u, EPI_REGLU, s); }
     if (c->rn_fused) {
         RowGemmArgs dn{};
-        dn.A = j->r8; dn.W = L.down_w; dn.Wf = L.down_wf; dn.M = M; dn.K = F; dn.d = d;
+        dn.A = r.r8; dn.W = L.down_w; dn.Wf = L.down_wf; dn.M = M; dn.K = F; dn.d = d;
         set_requant(dn, L.down_mult, L.down_shift);
         dn.w1 = L.post_ffn_norm; dn.w2 = next;
-        dn.x_in = j->x; dn.x_out = last ? nullptr : j->x; dn.xn = j->xn; dn.ws = j->rn_ws; dn.ws_bytes = j->rn_ws_bytes;
+        dn.x_in = r.x; dn.x_out = last ? nullptr : r.x; dn.xn = r.xn; dn.ws = r.rn_ws; dn.ws_bytes = r.rn_ws_bytes;
         { Timed t(c, "gemm_down_norm"); launch_gemm_rn(dn, s); }
     } else {
         GemmArgs dn{};
-        dn.A = j->r8; dn.W = L.down_w; dn.M = M; dn.N = d; dn.K = F; dn.out8 = j->y8; dn.ldo = d;
+        dn.A = r.r8; dn.W = L.down_w; dn.M = M; dn.N = d; dn.K = F; dn.out8 = r.y8; dn.ldo = d;
         set_requant(dn, L.down_mult, L.down_shift);
         { Timed t(c, "gemm_down"); launch_gemm(dn, EPI_REQ, s); }
-        { Timed t(c, "row_norm"); launch_resid_norm(j->x, j->y8, L.post_ffn_norm, next, M, d, j->xn, s); }
+        { Timed t(c, "row_norm"); launch_resid_norm(r.x, r.y8, L.post_ffn_norm, next, M, d, r.xn, s); }
     }
 }
 
@@ -621,7 +642,7 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T, bool head = t
         a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
         a.general = L.attn_general;
         { Timed t(c, "attention"); launch_attention(a, nb, s); }
-        post_attention(c, j, l, M);
+        post_attention(c, row_bufs(c, j), l, M, s);
     }
     if (head) {
         GemmArgs h{};
@@ -962,67 +983,141 @@ extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t* data, co
     return CZIP_OK;
 }
 
+// Streams of a group decoded as independent lanes (contiguous ranges of the
+// group, each on its own HIP stream): one lane's kernels fill the others'
+// partly empty last rounds of workgroups.  Two lanes measured best (three and
+// four lose to their smaller launches).  Not while per-kernel events are
+// recorded (they time one stream), nor for groups whose lanes would be small;
+// CZIP_DECODE_LANES=n (1..4) sets the number for every group.
+constexpr int DEC_LANES_MAX = 4;
+constexpr int DEC_LANE_MIN_STREAMS = 16384;
+constexpr int DEC_LANES_DEFAULT = 2;
+
+static int decode_lanes(const czip_ctx* c, int S) {
+    if (c->profiling) return 1;
+    if (const char* e = getenv("CZIP_DECODE_LANES")) {
+        const int n = atoi(e);
+        if (n >= 1 && n <= DEC_LANES_MAX) return std::min(n, S);
+    }
+    return std::max(1, std::min(DEC_LANES_DEFAULT, S / DEC_LANE_MIN_STREAMS));
+}
+
 static czip_status run_decompress(czip_job* j) {
     czip_ctx* c = j->ctx;
-    hipStream_t s = c->stream;
-    const int d = c->cfg.d_model, F = c->cfg.d_ff, V = c->cfg.vocab, H = c->cfg.n_heads;
+    const int d = c->cfg.d_model, V = c->cfg.vocab, H = c->cfg.n_heads;
     const int Tc = j->T;
     // KV caches per layer: K and V [S][KH][TP][64] (key-major); TP = the
     // longest stream rounded up to whole 64-key tiles
     const int TP = pad64(Tc);
-    const size_t layer_kv = (size_t)j->S * c->KH * TP * 64;
+    const size_t layer_kv = (size_t)j->S * c->KH * TP * 64, stream_kv = (size_t)c->KH * TP * 64;
     for (int64_t g0 = 0; g0 < j->nchunks; g0 += j->S) {
         const int S = (int)std::min<int64_t>(j->S, j->nchunks - g0);
+        const int nl = decode_lanes(c, S);
+        for (int ln = 1; ln < nl; ln++) {
+            if (c->lane_s[ln - 1]) continue;
+            if (hipStreamCreateWithFlags(&c->lane_s[ln - 1], hipStreamNonBlocking) != hipSuccess) {
+                c->lane_s[ln - 1] = nullptr;
+                return fail(c, CZIP_E_HIP, "hipStreamCreateWithFlags");
+            }
+        }
+        for (int e = 0; e < (nl > 1 ? nl : 0); e++) {
+            if (c->lane_ev[e]) continue;
+            if (hipEventCreateWithFlags(&c->lane_ev[e], hipEventDisableTiming) != hipSuccess) {
+                c->lane_ev[e] = nullptr;
+                return fail(c, CZIP_E_HIP, "hipEventCreateWithFlags");
+            }
+        }
+        struct Lane {
+            int r0, S;
+            hipStream_t s;
+            RowBufs r;
+            DecState st;
+            DecStreams ds;
+        };
+        Lane lanes[DEC_LANES_MAX];
+        for (int ln = 0; ln < nl; ln++) {
+            Lane& L = lanes[ln];
+            L.r0 = (int)((int64_t)S * ln / nl);
+            L.S = (int)((int64_t)S * (ln + 1) / nl) - L.r0;
+            L.s = ln == 0 ? c->stream : c->lane_s[ln - 1];
+            L.r = row_bufs(c, j, L.r0, nl, ln);
+            const size_t r0 = (size_t)L.r0;
+            L.st = DecState{j->st_low + r0, j->st_high + r0, j->st_code + r0, j->st_bpos + r0, j->st_bit + r0,
+                            j->st_plo + r0, j->st_phi + r0};
+            L.ds = DecStreams{j->d_data, j->d_offs + g0 + L.r0, j->d_blen + g0 + L.r0, j->d_ntok + g0 + L.r0,
+                              j->d_tokens, j->d_toff + g0 + L.r0};
+        }
         int steps = 0;
         for (int i = 0; i < S; i++) steps = std::max(steps, j->h_ntok[(size_t)(g0 + i)]);
-        DecState st{j->st_low, j->st_high, j->st_code, j->st_bpos, j->st_bit, j->st_plo, j->st_phi};
-        DecStreams ds{j->d_data, j->d_offs + g0, j->d_blen + g0, j->d_ntok + g0, j->d_tokens, j->d_toff + g0};
-        { Timed t(c, "dec_init"); launch_dec_init(st, ds, S, s); }
+        if (nl > 1) {  // the other lanes start after what the context's stream holds
+            HIPCHECK(c, hipEventRecord(c->lane_ev[0], c->stream));
+            for (int ln = 1; ln < nl; ln++) HIPCHECK(c, hipStreamWaitEvent(lanes[ln].s, c->lane_ev[0], 0));
+        }
+        for (int ln = 0; ln < nl; ln++) {
+            Timed t(c, "dec_init");
+            launch_dec_init(lanes[ln].st, lanes[ln].ds, lanes[ln].S, lanes[ln].s);
+        }
         for (int p = 0; p < steps; p++) {
-            {
-                Timed t(c, "dec_prep");
-                launch_dec_prep(ds, st, S, p, c->head_fused && p > 0, c->cfg.target_total, j->inp, s);
-            }
-            if (!c->rn_fused) { Timed t(c, "embed_norm"); launch_embed_norm(j->inp, c->embed, c->layers[0].attn_norm, S, d, j->x, j->xn, s); }
-            for (int l = 0; l < c->cfg.n_layers; l++) {
-                const DevLayer& L = c->layers[(size_t)l];
-                int8_t* kc = j->kc + (size_t)l * layer_kv;
-                int8_t* vc = j->vc + (size_t)l * layer_kv;
-                GemmArgs g{};
-                g.A = j->xn; g.W = L.qkv_w; g.M = S; g.N = L.qkv_n; g.K = d;
-                g.out8 = j->q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
-                g.d = d; g.T = TP; g.TP = TP; g.pos = p; g.vl = DEC_VL; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
-                g.KH = c->KH; g.kc = kc; g.vc = vc; g.rcos = c->rcos; g.rsin = c->rsin;
-                if (l == 0) {
-                    layer0_qkv(c, g, j->inp, s);
-                } else {
-                    Timed t(c, "gemm_qkv");
-                    launch_gemm(g, EPI_QKV, s);
+            for (int ln = 0; ln < nl; ln++) {
+                const Lane& Ln = lanes[ln];
+                const hipStream_t s = Ln.s;
+                const int M = Ln.S;
+                {
+                    Timed t(c, "dec_prep");
+                    launch_dec_prep(Ln.ds, Ln.st, M, p, c->head_fused && p > 0, c->cfg.target_total, Ln.r.inp, s);
                 }
-                AttnArgs a{};
-                a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = j->d_ntok + g0; a.score_mult = L.score_mult;
-                a.sink = L.sink; a.lut = c->lut; a.etab = c->etab; a.out = j->attn; a.M = S; a.T = TP; a.H = H; a.G = c->cfg.n_kv_heads;
-                a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;
-                a.general = L.attn_general;
-                { Timed t(c, "attn_decode"); launch_attn_decode(a, S, p, s); }
-                post_attention(c, j, l, S);
+                if (!c->rn_fused) {
+                    Timed t(c, "embed_norm");
+                    launch_embed_norm(Ln.r.inp, c->embed, c->layers[0].attn_norm, M, d, Ln.r.x, Ln.r.xn, s);
+                }
+                for (int l = 0; l < c->cfg.n_layers; l++) {
+                    const DevLayer& L = c->layers[(size_t)l];
+                    int8_t* kc = j->kc + (size_t)l * layer_kv + (size_t)Ln.r0 * stream_kv;
+                    int8_t* vc = j->vc + (size_t)l * layer_kv + (size_t)Ln.r0 * stream_kv;
+                    GemmArgs g{};
+                    g.A = Ln.r.xn; g.W = L.qkv_w; g.M = M; g.N = L.qkv_n; g.K = d;
+                    g.out8 = Ln.r.q8; g.ldo = d; set_requant(g, L.qkv_mult, L.qkv_shift);
+                    g.d = d; g.T = TP; g.TP = TP; g.pos = p; g.vl = DEC_VL; g.kv_mode = c->cfg.kv_mode; g.G = c->cfg.n_kv_heads;
+                    g.KH = c->KH; g.kc = kc; g.vc = vc; g.rcos = c->rcos; g.rsin = c->rsin;
+                    if (l == 0) {
+                        layer0_qkv(c, g, Ln.r.inp, s);
+                    } else {
+                        Timed t(c, "gemm_qkv");
+                        launch_gemm(g, EPI_QKV, s);
+                    }
+                    AttnArgs a{};
+                    a.q = Ln.r.q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = Ln.ds.ntok; a.score_mult = L.score_mult;
+                    a.sink = L.sink; a.lut = c->lut; a.etab = c->etab; a.out = Ln.r.attn; a.M = M; a.T = TP; a.H = H;
+                    a.G = c->cfg.n_kv_heads; a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;
+                    a.general = L.attn_general;
+                    { Timed t(c, "attn_decode"); launch_attn_decode(a, M, p, s); }
+                    post_attention(c, Ln.r, l, M, s);
+                }
+                if (c->head_fused) {
+                    HeadDecArgs h{};
+                    h.A = Ln.r.xn; h.W = c->head_wf; h.M = M; h.K = d; h.V = V;
+                    h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total; h.p = p;
+                    Timed t(c, "head_dec");
+                    launch_head_dec(h, Ln.st, Ln.ds, s);
+                } else {
+                    GemmArgs hd{};
+                    hd.A = Ln.r.xn; hd.W = c->head_w; hd.M = M; hd.N = V; hd.K = d;
+                    hd.out32 = j->logits + (size_t)Ln.r0 * V; hd.ldo = V;
+                    { Timed t(c, "gemm_head"); launch_gemm(hd, EPI_RAW, s); }
+                    {
+                        Timed t(c, "cdf_decode");
+                        launch_cdf_decode(hd.out32, M, V, c->lut, c->cfg.coef_q24, c->cfg.target_total, p, Ln.st, Ln.ds, s);
+                    }
+                }
             }
-            if (c->head_fused) {
-                HeadDecArgs h{};
-                h.A = j->xn; h.W = c->head_wf; h.M = S; h.K = d; h.V = V;
-                h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total; h.p = p;
-                Timed t(c, "head_dec");
-                launch_head_dec(h, st, ds, s);
-            } else {
-                GemmArgs hd{};
-                hd.A = j->xn; hd.W = c->head_w; hd.M = S; hd.N = V; hd.K = d; hd.out32 = j->logits; hd.ldo = V;
-                { Timed t(c, "gemm_head"); launch_gemm(hd, EPI_RAW, s); }
-                { Timed t(c, "cdf_decode"); launch_cdf_decode(j->logits, S, V, c->lut, c->cfg.coef_q24, c->cfg.target_total, p, st, ds, s); }
-            }
+        }
+        for (int ln = 1; ln < nl; ln++) {  // the next group (and the caller) see every lane done
+            HIPCHECK(c, hipEventRecord(c->lane_ev[ln], lanes[ln].s));
+            HIPCHECK(c, hipStreamWaitEvent(c->stream, c->lane_ev[ln], 0));
         }
     }
     HIPCHECK(c, hipGetLastError());
-    HIPCHECK(c, hipStreamSynchronize(s));
+    HIPCHECK(c, hipStreamSynchronize(c->stream));
     resolve_events(c);
     return CZIP_OK;
 }
@@ -1161,7 +1256,7 @@ extern "C" czip_status czip_decode_step(czip_ctx* c, const uint32_t* tok_in, con
         a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;  // ATTN_COEF_Q24 (attention.rs:17-19)
         a.general = L.attn_general;
         { Timed t(c, "attn_decode"); launch_attn_decode(a, S, p, s); }
-        post_attention(c, j, l, S);
+        post_attention(c, row_bufs(c, j), l, S, s);
     }
     {
         GemmArgs hd{};

@@ -372,6 +372,26 @@ def test_decompress_stream_groups(gpu_shipped, shipped, monkeypatch):
     assert np.array_equal(out, toks)
 
 
+@pytest.mark.parametrize("lanes,fused", [(2, True), (2, False), (4, True)])
+def test_decompress_lanes(amd, shipped, monkeypatch, lanes, fused):
+    """A group's streams decoded as several lanes on their own HIP streams
+    (forced on for small groups): odd group sizes, a last group of three (fewer
+    streams than lanes), ragged streams; with the fused kernels and with the
+    separate norm / FFN / LM head kernels."""
+    monkeypatch.setenv("CZIP_DECODE_LANES", str(lanes))
+    monkeypatch.setenv("CZIP_DECODE_STREAMS", "5")
+    if not fused:
+        for k in ("CZIP_UNFUSED_NORM", "CZIP_UNFUSED_HEAD", "CZIP_UNFUSED_FFN"):
+            monkeypatch.setenv(k, "1")
+    gm = amd.Model(amd.ModelWeights(MODEL_PATH))
+    rng = np.random.default_rng(71)
+    ntoks = [64] * 12 + [23]
+    toks = rng.integers(0, 1024, sum(ntoks)).astype(np.uint32)
+    chunks = shipped.compress_many(toks, 64, threads=8)
+    _say(f"decompress {lanes} lanes, fused {fused}")
+    assert np.array_equal(gm.decompress_chunks(chunks, ntoks), toks)
+
+
 @pytest.mark.parametrize("kv", ["compat", "gqa"])
 def test_config_d512_l8_full_shape(amd, orc, tmp_path, kv):
     """The d512 / 8-layer / 8 heads, 2 KV heads / F 2048 / V 1024 configuration
