@@ -362,6 +362,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
     int nmax = nrow;
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
+    nmax = __builtin_amdgcn_readfirstlane(nmax);  // every lane holds the max over the 16 rows
     // A operand of the PV product, and the sum over the tile's KT keys (of
     // every stream) of v at head dim = lane: rows of ones times V, whose
     // output lane l holds column l % 16, i.e. dim 16 db + l % 16
@@ -426,8 +427,9 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
             rhi = rlo ? rhi : rhi & (rhi - 1u);
             rlo &= rlo - 1u;
         }
-        // 4a. S of this lane's row (lanes = rows): rescale at record j, then add segment j
-        if (erow) st.S = rescale_s(st.S, erow);
+        // 4a. S of this lane's row (lanes = rows): rescale at record j (a
+        // factor of 65536 leaves S as it is), then add segment j
+        st.S = rescale_s(st.S, erow ? erow : 65536u);
         st.S += (unsigned)sw + (unsigned)KT * WOFF;
         // the high- and low-byte products of two head-dim blocks at a time are
         // independent, so their MFMAs issue back to back and one shift-add
