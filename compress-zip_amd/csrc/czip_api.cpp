@@ -84,6 +84,7 @@ struct czip_ctx {
     bool rn_fused = false;  // residual + norms fused into the row GEMM (gemm_rn_supported(d_model))
     bool head_fused = false;  // LM head fused with the coder interval stage / decode step (head_cdf_supported(vocab))
     bool ffn_fused = false;   // up + ReGLU + down + norms in one kernel (ffn_supported(d_model, d_ff))
+    int64_t ffn_min_rows = FFN_MIN_ROWS;  // rows from which it is used (CZIP_FFN_MIN_ROWS)
     std::vector<void*> allocs;
     int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr, *head_wf = nullptr;
     int8_t* embed_xn = nullptr;  // rmsnorm(embed[v], layer 0's attn_norm) for every token v
@@ -352,6 +353,7 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
     c->rn_fused = gemm_rn_supported(w->d_model) && getenv("CZIP_UNFUSED_NORM") == nullptr;
     c->head_fused = head_cdf_supported(w->vocab) && w->coef_q24 < (1u << 23) && getenv("CZIP_UNFUSED_HEAD") == nullptr;
     c->ffn_fused = c->rn_fused && ffn_supported(w->d_model, w->d_ff) && getenv("CZIP_UNFUSED_FFN") == nullptr;
+    if (const char* e = getenv("CZIP_FFN_MIN_ROWS")) c->ffn_min_rows = std::max(1ll, atoll(e));
     czip_ctx* C = c.get();
 #define UP(dst, src, n) if ((rc = upload(C, &dst, src, n))) return rc;
     UP(c->embed, w->embed, V * d)
@@ -558,7 +560,7 @@ void post_attention(czip_ctx* c, const RowBufs& r, int l, int M, hipStream_t s) 
     // the fused FFN walks 128-row strips with one workgroup per CU: it pays
     // off for prefill sub-batches, while a decode step's few thousand rows
     // balance better over the separate kernels' 64-row blocks
-    if (c->ffn_fused && M >= FFN_MIN_ROWS) {
+    if (c->ffn_fused && M >= c->ffn_min_rows) {
         GemmArgs u{}, dn{};  // requantization parameters of the two products
         u.K = d; set_requant(u, L.up_mult, L.up_shift);
         dn.K = F; set_requant(dn, L.down_mult, L.down_shift);

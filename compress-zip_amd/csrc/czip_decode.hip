@@ -573,21 +573,19 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
     for (int i = 0; i < 4; i++) {
         const int rr = i * 16 + lr;
         const unsigned v = row_v[rr], rem = row_rem[rr];
-        const int am = L.row_am[rr];
+        // the argmax as (tile, element) of this lane's 4-column groups, if it is one of them
+        const int amk = L.row_am[rr] - (nb + c4);
+        const int am_t = amk >= 0 && (amk & 15) < 4 ? amk >> 4 : -1;
         unsigned run = L.red_c[wave][rr];
-        // the lane's 4-column group of tile t holding v, if any: kept in
-        // registers, one store per row
-        int fsym = -1;
-        unsigned flo = 0u, fhi = 0u;
+        // per tile, only the group sum (the argmax's group with the
+        // remainder) and its start: the one group of the row holding v is
+        // kept and searched after the loop
+        int ht = -1;
+        unsigned hb0 = 0u;
 #pragma unroll
         for (int t = 0; t < CT; t++) {
-            unsigned f[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int col = nb + t * 16 + c4 + r;
-                f[r] = (unsigned)acc[i][t][r] + (col == am ? rem : 0u);
-            }
-            const unsigned g = f[0] + f[1] + f[2] + f[3];
+            const unsigned g = (unsigned)acc[i][t][0] + (unsigned)acc[i][t][1] + (unsigned)acc[i][t][2] +
+                               (unsigned)acc[i][t][3] + (am_t == t ? rem : 0u);
             // inclusive prefix over the four lane groups of the row, and their total
             unsigned x = g;
             const unsigned y1 = (unsigned)__shfl_up((int)x, 16, 64);
@@ -595,19 +593,27 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
             const unsigned y2 = (unsigned)__shfl_up((int)x, 32, 64);
             x += grp >= 2 ? y2 : 0u;
             const unsigned tile_sum = (unsigned)__shfl((int)x, lr + 48, 64);
-            // cumulative bounds of the group's columns: [b0, b1), [b1, b2), ...
-            const unsigned b0 = run + x - g, b1 = b0 + f[0], b2 = b1 + f[1], b3 = b2 + f[2], b4 = b3 + f[3];
-            const unsigned k = (v >= b1 ? 1u : 0u) + (v >= b2 ? 1u : 0u) + (v >= b3 ? 1u : 0u);
-            const bool in = b0 <= v && v < b4;  // every f >= 1: at most one column holds v
-            fsym = in ? nb + t * 16 + c4 + (int)k : fsym;
-            flo = in ? (k == 0 ? b0 : k == 1 ? b1 : k == 2 ? b2 : b3) : flo;
-            fhi = in ? (k == 0 ? b1 : k == 1 ? b2 : k == 2 ? b3 : b4) : fhi;
+            const unsigned b0 = run + x - g;
+            const bool in = v - b0 < g;  // b0 <= v < b0 + g; every f >= 1: at most one group holds v
+            ht = in ? t : ht;
+            hb0 = in ? b0 : hb0;
             run += tile_sum;
         }
-        if (fsym >= 0) {
-            row_sym[rr] = fsym;
-            row_lo[rr] = flo;
-            row_hi[rr] = fhi;
+        if (ht >= 0) {
+            // the held group's frequencies (the argmax's with the remainder)
+            unsigned f[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                unsigned e = (unsigned)acc[i][0][r];
+#pragma unroll
+                for (int t = 1; t < CT; t++) e = ht == t ? (unsigned)acc[i][t][r] : e;
+                f[r] = e + (am_t == ht && (amk & 3) == r ? rem : 0u);
+            }
+            const unsigned b1 = hb0 + f[0], b2 = b1 + f[1], b3 = b2 + f[2];
+            const unsigned k = (v >= b1 ? 1u : 0u) + (v >= b2 ? 1u : 0u) + (v >= b3 ? 1u : 0u);
+            row_sym[rr] = nb + ht * 16 + c4 + (int)k;
+            row_lo[rr] = k == 0 ? hb0 : k == 1 ? b1 : k == 2 ? b2 : b3;
+            row_hi[rr] = k == 0 ? b1 : k == 1 ? b2 : k == 2 ? b3 : b3 + f[3];
         }
     }
     __syncthreads();
@@ -622,10 +628,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
 
 void launch_head_dec(const HeadDecArgs& a, DecState st, DecStreams ds, hipStream_t s) {
     dim3 grid((unsigned)((a.M + HBM_ROWS - 1) / HBM_ROWS));
-    switch (a.V) {
-        case 512: hipLaunchKernelGGL(k_head_dec<2>, grid, dim3(64 * HNW), 0, s, a, st, ds); break;
-        default: hipLaunchKernelGGL(k_head_dec<4>, grid, dim3(64 * HNW), 0, s, a, st, ds); break;
-    }
+    hipLaunchKernelGGL(k_head_dec<4>, grid, dim3(64 * HNW), 0, s, a, st, ds);
 }
 
 }  // namespace czip

@@ -80,14 +80,14 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
     }
 }
 
-bool head_cdf_supported(int V) { return V == 512 || V == 1024; }
+// V = 1024 (16 waves x 4 tiles of 16 columns): the fused heads serve the
+// coder paths, which feed BOS = 1022 and so need V > 1022; other vocabularies
+// take the LM head GEMM + k_cdf
+bool head_cdf_supported(int V) { return V == 1024; }
 
 void launch_head_cdf(const HeadCdfArgs& a, hipStream_t s) {
     dim3 grid((unsigned)((a.M + HBM_ROWS - 1) / HBM_ROWS));
-    switch (a.V) {
-        case 512: hipLaunchKernelGGL(k_head_cdf<2>, grid, dim3(64 * HNW), 0, s, a); break;
-        default: hipLaunchKernelGGL(k_head_cdf<4>, grid, dim3(64 * HNW), 0, s, a); break;
-    }
+    hipLaunchKernelGGL(k_head_cdf<4>, grid, dim3(64 * HNW), 0, s, a);
 }
 
 }  // namespace czip

@@ -124,7 +124,7 @@ bool ffn_supported(int d, int F);
 void launch_ffn(const FfnArgs& a, hipStream_t s);
 
 // LM head + logits -> (cum_lo, cum_hi) of each row's target (k_cdf mode 0)
-// without the int32 logits leaving the chip; V in {512, 1024}.
+// without the int32 logits leaving the chip; V = 1024.
 struct HeadCdfArgs {
     const int8_t* A;           // [M, K] final-normalized rows
     const int8_t* W;           // [V, K] head weights, fragment-major (rowblock_mma)

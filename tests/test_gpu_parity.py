@@ -213,6 +213,25 @@ def test_unfused_ffn_path(gpu_shipped, shipped, monkeypatch, amd):
     assert np.array_equal(gm.decompress_chunks(ref, lens), toks)
 
 
+@pytest.mark.parametrize("chunk,n_chunks", [(512, 3), (96, 350)])
+def test_fused_ffn_small_launches(amd, shipped, monkeypatch, chunk, n_chunks):
+    """The fused FFN kernel (used from 2^19 rows) forced onto small launches:
+    1,536 rows, and 33,600 rows = 262.5 strips of 128 (a partial last strip,
+    more strips than the 256 workgroups, so some take a second strip with the
+    next strip's input prefetched); the compressed bytes against the oracle's,
+    and the decode, whose steps then run it too."""
+    monkeypatch.setenv("CZIP_FFN_MIN_ROWS", "1")
+    gm = amd.Model(amd.ModelWeights(MODEL_PATH))
+    rng = np.random.default_rng(80 + chunk)
+    n = chunk * n_chunks - chunk // 3
+    toks = rng.integers(0, 1024, n).astype(np.uint32)
+    ref = shipped.compress_many(toks, chunk, threads=8)
+    _say(f"fused FFN forced, chunk={chunk} chunks={n_chunks}")
+    assert gm.compress_chunks(toks, chunk) == ref
+    ntoks = [min(chunk, n - chunk * c) for c in range(len(ref))]
+    assert np.array_equal(gm.decompress_chunks(ref, ntoks), toks)
+
+
 def test_requant_general_path(amd, orc, tmp_path):
     """Requantization outside the GEMMs' f64 fast path (|mult| >= 2^26, negative
     multipliers, shift <= 0) against the oracle."""
