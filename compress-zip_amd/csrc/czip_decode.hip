@@ -509,23 +509,25 @@ void launch_cdf_decode(const int32_t* logits, int S, int V, const uint16_t* lut,
 //     remainder) and value = ((code - low + 1) * total - 1) / range, clamped
 //     to total - 1 (a value >= total decodes as the last symbol, whose
 //     interval ends at total: arith_coder.rs:225-241);
-//   - every lane scans its columns in column order (tile, lane group, element)
-//     from its wave's base, the lane-group prefix within a tile by two
-//     shuffles; the one column with lo <= value < hi is the symbol;
-//   - wave 0 narrows the interval and renormalizes (arith_coder.rs:243-262)
-//     reading bits from an 8-byte window of the stream (a step shifts at most
-//     32 bits: each pass shifts a 0 into low and a 1 into high, and after 32
-//     of them low = 0, high = 2^32 - 1 ends the loop).
+//   - every lane walks its 4-column groups in column order (tile, lane
+//     group) from its wave's base, the lane-group prefix within a tile by two
+//     shuffles, and keeps the one group whose range holds the value; that
+//     group's columns give the symbol (the one column with lo <= value < hi)
+//     and its interval;
+//   - wave 0 stores the symbol and the interval; the next step's input
+//     kernel narrows and renormalizes the decoder (arith_coder.rs:243-262).
 // ---------------------------------------------------------------------------
 template <int CT>
 __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState st, DecStreams ds) {
-    __shared__ HeadLds L;
+    __shared__ HeadLdsT<1> L;
     __shared__ unsigned row_v[HBM_ROWS], row_rem[HBM_ROWS], row_lo[HBM_ROWS], row_hi[HBM_ROWS];
     __shared__ int row_sym[HBM_ROWS];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int m0 = blockIdx.x * HBM_ROWS;
     const int nb = wave * CT * 16;
     const int lr = lane & 15, grp = lane >> 4, c4 = grp * 4;
+    const int m0 = blockIdx.x * HBM_ROWS;
+    head_stage_a(a.A, a.M, a.K, m0, L.As[0]);
+    head_etab_fill(L, a.lut);
     // decoder state of wave 0's stream, requested before the GEMM
     const int b = m0 + lane;
     bool live = false;
@@ -536,8 +538,10 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
         high = st.high[b];
         code = st.code[b];
     }
+    __builtin_amdgcn_s_waitcnt(0);  // the block's A (and everything before) has landed
+    __syncthreads();
     v4i acc[4][CT];
-    head_freqs<CT>(a.A, a.M, a.K, a.W, a.V, m0, a.lut, a.coef, a.total, L, acc);
+    head_freqs<CT>(tid, L.As[0], a.K, a.W, a.V, a.coef, a.total, L, acc);
     // sum f per row and wave
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -626,6 +630,9 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
     st.pend_hi[b] = row_hi[lane];
 }
 
+// One workgroup per 64-stream block (not persistent like the compress head:
+// with two decode lanes sharing the GPU, blocks handed to whichever CU frees
+// up finish sooner than a fixed share per workgroup)
 void launch_head_dec(const HeadDecArgs& a, DecState st, DecStreams ds, hipStream_t s) {
     dim3 grid((unsigned)((a.M + HBM_ROWS - 1) / HBM_ROWS));
     hipLaunchKernelGGL(k_head_dec<4>, grid, dim3(64 * HNW), 0, s, a, st, ds);

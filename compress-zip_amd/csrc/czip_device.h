@@ -109,6 +109,39 @@ __device__ __forceinline__ void rowblock_mma(const int8_t* A, int M, int K, cons
     if (kt < nk) step(kt, w0, w1);
 }
 
+// The K steps of rowblock_mma_full over a row block already in As (its
+// caller staged it and waited for every wave): each wave's W one step ahead.
+template <int CT>
+__device__ __forceinline__ void rowblock_mma_lds(int lane, int K, const int8_t* Wf, int wrows, int nb,
+                                                 const int8_t (*As)[64 * 64], v4i (&acc)[4][CT]) {
+    const int lr = lane & 15;
+    const int nkt = K / 64;
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)Wf, (short)0, wrows * K, BUF_DWORD3);
+    const int woff = (nb >> 4) * nkt * 1024 + lane * 16;
+    v4i w0[CT], w1[CT];
+    auto fetch_w = [&](v4i* w, int kt) {
+#pragma unroll
+        for (int t = 0; t < CT; t++) w[t] = __builtin_amdgcn_raw_buffer_load_b128(rW, woff + t * nkt * 1024, kt * 1024, 0);
+    };
+    fetch_w(w0, 0);
+    auto step = [&](int kt, const v4i* wc, v4i* wn) {
+        if (kt + 1 < nkt) fetch_w(wn, kt + 1);
+        v4i af[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[i] = *(const v4i*)(As[kt] + lds64(i * 16 + lr, lane >> 4));
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int t = 0; t < CT; t++) acc[i][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wc[t], af[i], acc[i][t], 0, 0, 0);
+    };
+    int kt = 0;
+    for (; kt + 1 < nkt; kt += 2) {
+        step(kt, w0, w1);
+        step(kt + 1, w1, w0);
+    }
+    if (kt < nkt) step(kt, w0, w1);
+}
+
 // The same product with the row block's whole A (64 rows x K) staged in LDS
 // at once (As: K / 64 tiles of [64][64], 64-byte permuted rows), one barrier,
 // then the K steps without barriers, each wave's W one step ahead.  The

@@ -20,9 +20,14 @@ constexpr int HBM_ROWS = 64, HNW = 16;
 // whatever lut[0] holds).
 constexpr int ETAB_N = 4098;
 
+constexpr int HEAD_GRID = 256;   // persistent head kernels: one workgroup (16 waves, 4 per SIMD) per CU
 constexpr int HEAD_KMAX = 1024;  // the whole K of a row block staged at once (d_model <= 1024)
-struct HeadLds {
-    int8_t As[HEAD_KMAX / 64][HBM_ROWS * 64] __attribute__((aligned(16)));
+// NA row blocks of A (K / 64 tiles of [64][64], 64-byte permuted rows): the
+// persistent compress head holds two (the one being multiplied and the next
+// one arriving), the decode head one
+template <int NA>
+struct HeadLdsT {
+    int8_t As[NA][HEAD_KMAX / 64][HBM_ROWS * 64] __attribute__((aligned(16)));
     unsigned etab[ETAB_N + 2];
     int red_a[HNW][HBM_ROWS];
     unsigned red_b[HNW][HBM_ROWS], red_c[HNW][HBM_ROWS];
@@ -31,7 +36,46 @@ struct HeadLds {
     double row_y[HBM_ROWS];
 };
 
-// Logits of the block (rowblock_mma_full), then per row, with two block reductions:
+// The exp table of head_freqs, built once per workgroup.
+template <class Lds>
+__device__ __forceinline__ void head_etab_fill(Lds& L, const uint16_t* lut) {
+    for (int t = threadIdx.x; t < ETAB_N; t += 64 * HNW) {
+        const unsigned ip = (unsigned)t >> 8;
+        const unsigned x = ip >= 16u ? 1u : ((65536u >> ip) * (unsigned)lut[t & 255] + 0x8000u) >> 16;
+        L.etab[t] = t == ETAB_N - 1 ? 65535u : (x < 1u ? 1u : (x > 65535u ? 65535u : x));
+    }
+}
+
+// threadIdx.x with a value the compiler cannot follow across loop iterations
+__device__ __forceinline__ int opaque_tid() {
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+// Requests the 64 x K block of A at row m0 into As by LDS DMA (no registers
+// held; rows past M read as 0): each wave instruction fills 1 KB, the 16 rows
+// 16 (q % 4) .. +16 of K step q / 4, lane l writing the 16 bytes at l * 16,
+// i.e. row 16 (q % 4) + l / 4, slot l % 4 of the permuted row (lds64), which
+// holds the row's 16-byte piece (l % 4) ^ ((row >> 1) & 3).  The caller waits
+// for the loads (s_waitcnt) and then for every wave (a barrier).
+__device__ __forceinline__ void head_stage_a(const int8_t* A, int M, int K, int m0, int8_t (*As)[HBM_ROWS * 64]) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int arows = M - m0 < HBM_ROWS ? M - m0 : HBM_ROWS;
+    const __amdgpu_buffer_rsrc_t rA =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(A + (size_t)m0 * K), (short)0, arows * K, BUF_DWORD3);
+    for (int q = wave; q < (K / 64) * 4; q += HNW) {
+        const int kt = q >> 2, row = (q & 3) * 16 + (lane >> 2);
+        const int piece = (lane & 3) ^ ((row >> 1) & 3);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (__attribute__((address_space(3))) void*)(As[kt] + (q & 3) * 1024), 16,
+                                                 row * K + kt * 64 + piece * 16, 0, 0, 0);
+    }
+}
+
+// Logits of a row block staged in As (its K steps from LDS, each wave's W
+// columns one step ahead in registers), then per row, with two block
+// reductions:
 //   1. max logit;
 //   2. first argmax (row_am) and S = sum E(l - max) (softmax_cdf.rs:96-110,
 //      coef < 2^24);
@@ -42,23 +86,20 @@ struct HeadLds {
 // its error is < 2^16 * 2^-54 + 2^-37 < 2^-36, while a nonzero fraction of
 // e*Rm/S is >= 1/S >= 2^-26 (S < 2^26).  The argmax's remainder
 // (total - sum f) is left to the caller.
-template <int CT>
-__device__ __forceinline__ void head_freqs(const int8_t* A, int M, int K, const int8_t* W, int V, int m0,
-                                           const uint16_t* lut, unsigned coef, unsigned total, HeadLds& L,
-                                           v4i (&acc)[4][CT]) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+// tid: threadIdx.x, passed in so that a persistent caller can make it opaque
+// per block (the lane-dependent addresses are then formed per block instead
+// of being held in registers across the whole loop).
+template <int CT, class Lds>
+__device__ __forceinline__ void head_freqs(int tid, const int8_t (*As)[HBM_ROWS * 64], int K, const int8_t* W, int V,
+                                           unsigned coef, unsigned total, Lds& L, v4i (&acc)[4][CT]) {
+    const int wave = tid >> 6, lane = tid & 63;
     const int nb = wave * CT * 16;
     const int lr = lane & 15, c4 = (lane >> 4) * 4;
-    for (int t = tid; t < ETAB_N; t += 64 * HNW) {
-        const unsigned ip = (unsigned)t >> 8;
-        const unsigned x = ip >= 16u ? 1u : ((65536u >> ip) * (unsigned)lut[t & 255] + 0x8000u) >> 16;
-        L.etab[t] = t == ETAB_N - 1 ? 65535u : (x < 1u ? 1u : (x > 65535u ? 65535u : x));
-    }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int t = 0; t < CT; t++) acc[i][t] = (v4i){0, 0, 0, 0};
-    rowblock_mma_full<CT>(A, M, K, W, V, m0, nb, L.As, acc);
+    rowblock_mma_lds<CT>(lane, K, W, V, nb, As, acc);
 
     // 1. row max
 #pragma unroll
