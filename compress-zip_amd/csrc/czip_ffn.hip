@@ -3,8 +3,9 @@
 // post-FFN RMSNorm + residual add, and the next pre-norm, on int8 MFMA.
 //
 // A workgroup of 8 waves walks strips of R = 16 RT rows.  The strip's
-// normalized input (R x d bytes) sits in LDS for the whole strip; the F
-// features go by in chunks of 128 (16 per wave):
+// normalized input (R x d bytes) sits in LDS for the whole strip, the next
+// strip's arriving in a second buffer by LDS DMA; the F features go by in
+// chunks of 128 (16 per wave):
 //   * up: each wave multiplies the strip by its 16 gate and 16 up weight rows
 //     (register-resident for the chunk, fragment-major with gate and up tiles
 //     interleaved per 16 features), applies requant + ReGLU and writes the
@@ -32,9 +33,9 @@ __global__ __launch_bounds__(64 * FFN_NW, 1) void k_ffn(FfnArgs a) {
     constexpr int R = 16 * RT;           // rows per strip
     constexpr int D = FFN_NW * CT * 16;  // d_model
     constexpr int KS = D / 64;           // K steps of the up projection
-    constexpr int NP = R * D / 16 / (64 * FFN_NW);  // 16-byte pieces of the strip per thread
-    static_assert(R * D / 16 % (64 * FFN_NW) == 0, "strip pieces per thread");
-    __shared__ __attribute__((aligned(16))) int8_t xs[KS * R * 64];    // KS tiles of [R][64]: the strip's input
+    // two strips' input, KS tiles of [R][64] each: the current strip's, and
+    // the next one's arriving by LDS DMA
+    __shared__ __attribute__((aligned(16))) int8_t xs[2][KS * R * 64];
     __shared__ __attribute__((aligned(16))) int8_t rs[2][2 * R * 64];  // 2 tiles of [R][64]: a chunk's ReGLU bytes
     __shared__ unsigned red[FFN_NW][R];
     __shared__ int inv_s[R];
@@ -52,7 +53,6 @@ __global__ __launch_bounds__(64 * FFN_NW, 1) void k_ffn(FfnArgs a) {
 
     v4i wu[2][KS];    // gate / up operands of the wave's 16 features of the current chunk
     v4i wd[CT][2];    // down operands of the wave's CT column tiles, the chunk's two K steps
-    v4i xr[NP];       // the next strip's input on its way to LDS
     auto load_wu = [&](int c) {
         const int g = c * FFN_NW + wave;
 #pragma unroll
@@ -67,22 +67,21 @@ __global__ __launch_bounds__(64 * FFN_NW, 1) void k_ffn(FfnArgs a) {
             for (int k = 0; k < 2; k++)
                 wd[i][k] = __builtin_amdgcn_raw_buffer_load_b128(rWd, lane * 16, ((wave * CT + i) * FK + 2 * c + k) * 1024, 0);
     };
-    // piece p = tid + 512 n: row p / (D / 16), 16-byte column chunk p % (D / 16)
-    auto load_x = [&](int s) {
+    // strip s's input into xs[b] by LDS DMA (no registers held; rows past M
+    // read as 0): a wave instruction fills the 16 rows 16 (q % (R / 16)) .. +16
+    // of K step q / (R / 16), lane l the 16 bytes at l * 16 (row + l / 4, slot
+    // l % 4 of the permuted row, which holds piece (l % 4) ^ ((row >> 1) & 3))
+    auto stage_x = [&](int s, int b) {
         const int m0 = s * R;
         const __amdgpu_buffer_rsrc_t rX =
             __builtin_amdgcn_make_buffer_rsrc((void*)(a.xn + (size_t)m0 * D), (short)0, min(a.M - m0, R) * D, BUF_DWORD3);
 #pragma unroll
-        for (int n = 0; n < NP; n++) {
-            const int p = tid + 64 * FFN_NW * n;
-            xr[n] = __builtin_amdgcn_raw_buffer_load_b128(rX, (p / (D / 16)) * D + (p % (D / 16)) * 16, 0, 0);
-        }
-    };
-    auto store_x = [&]() {
-#pragma unroll
-        for (int n = 0; n < NP; n++) {
-            const int p = tid + 64 * FFN_NW * n, row = p / (D / 16), c16 = p % (D / 16);
-            *(v4i*)(xs + (c16 >> 2) * R * 64 + lds64(row, c16 & 3)) = xr[n];
+        for (int q = wave; q < KS * (R / 16); q += FFN_NW) {
+            const int ks = q / (R / 16), rq = q % (R / 16);
+            const int row = rq * 16 + (lane >> 2), piece = (lane & 3) ^ ((row >> 1) & 3);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rX, (__attribute__((address_space(3))) void*)(xs[b] + ks * R * 64 + rq * 1024), 16,
+                row * D + ks * 64 + piece * 16, 0, 0, 0);
         }
     };
 
@@ -93,11 +92,11 @@ __global__ __launch_bounds__(64 * FFN_NW, 1) void k_ffn(FfnArgs a) {
         w1r[i] = *(const unsigned*)(a.w1 + nb + i * 16 + c4);
         w2r[i] = *(const unsigned*)(a.w2 + nb + i * 16 + c4);
     }
-    load_x(blockIdx.x);
+    stage_x(blockIdx.x, 0);
     load_wu(0);
-    store_x();
 
-    for (int s = blockIdx.x; s < nstrips; s += gridDim.x) {
+    int xb = 0;  // xs buffer of the current strip
+    for (int s = blockIdx.x; s < nstrips; s += gridDim.x, xb ^= 1) {
         const int m0 = s * R;
         const bool more = s + (int)gridDim.x < nstrips;
         v4i acc[RT][CT];
@@ -106,7 +105,10 @@ __global__ __launch_bounds__(64 * FFN_NW, 1) void k_ffn(FfnArgs a) {
 #pragma unroll
             for (int i = 0; i < CT; i++) acc[rt][i] = (v4i){0, 0, 0, 0};
 
-        __syncthreads();  // the strip's input is in LDS
+        __builtin_amdgcn_s_waitcnt(0);  // the strip's input (and everything before) has landed
+        __syncthreads();
+        if (more) stage_x(s + gridDim.x, xb ^ 1);  // its buffer was last read by the previous strip
+        const int8_t* const xsb = xs[xb];
         for (int c = 0; c < NC; c++) {
             int8_t* rb = rs[c & 1];
             load_wd(c);
@@ -116,8 +118,8 @@ __global__ __launch_bounds__(64 * FFN_NW, 1) void k_ffn(FfnArgs a) {
                 v4i ug0 = {0, 0, 0, 0}, uu0 = {0, 0, 0, 0}, ug1 = {0, 0, 0, 0}, uu1 = {0, 0, 0, 0};
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++) {
-                    const v4i a0 = *(const v4i*)(xs + ks * R * 64 + lds64(rt * 16 + lr, lg));
-                    const v4i a1 = *(const v4i*)(xs + ks * R * 64 + lds64(rt * 16 + 16 + lr, lg));
+                    const v4i a0 = *(const v4i*)(xsb + ks * R * 64 + lds64(rt * 16 + lr, lg));
+                    const v4i a1 = *(const v4i*)(xsb + ks * R * 64 + lds64(rt * 16 + 16 + lr, lg));
                     ug0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wu[0][ks], a0, ug0, 0, 0, 0);
                     uu0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wu[1][ks], a0, uu0, 0, 0, 0);
                     ug1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wu[0][ks], a1, ug1, 0, 0, 0);
@@ -179,7 +181,6 @@ __global__ __launch_bounds__(64 * FFN_NW, 1) void k_ffn(FfnArgs a) {
             __syncthreads();
         };
         row_inv();
-        if (more) load_x(s + gridDim.x);  // every wave is past the strip's last up phase
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
             const int row = m0 + rt * 16 + lr;
@@ -214,10 +215,7 @@ __global__ __launch_bounds__(64 * FFN_NW, 1) void k_ffn(FfnArgs a) {
         }
         __syncthreads();
         row_inv();
-        if (more) {
-            store_x();  // read by the next strip after its first barrier
-            load_wu(0);
-        }
+        if (more) load_wu(0);
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
             const int row = m0 + rt * 16 + lr;
