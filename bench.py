@@ -27,15 +27,15 @@ PEAK_HBM_GBS = 8000.0       # GB/s
 # HBM bytes per token (read + write) of each kernel on the text workload, from
 # two rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0: the factors a
 # plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text.md
-TRAFFIC_B_PER_TOKEN = {"attention": 516 + 411, "qkv_table": 12 + 512, "gemm_o_norm": 396 + 1152,
-                       "ffn": 1584 + 385, "gemm_down_norm": 1814 + 384, "gemm_up": 556 + 1024, "head_cdf": 390 + 8}
+TRAFFIC_B_PER_TOKEN = {"attention": 518 + 467, "qkv_table": 12 + 512, "gemm_o_norm": 396 + 1152,
+                       "ffn": 1441 + 384, "gemm_down_norm": 1946 + 384, "gemm_up": 677 + 1024, "head_cdf": 390 + 8}
 TRAFFIC_WORKLOADS = ("v001_L4_ctx512_text64MiB",)
 # Prefill attention: wave64 VALU instructions (MFMA excluded) per 16-row tile (64 keys, or
 # 32 for a row block's last tile when its visible keys end in the first half), from
 # SQ_INSTS_VALU - SQ_INSTS_VALU_MFMA_I8 on the same workload
 # (profiles/counters_compress_v001_ctx512_text8Mtok.md); the VALU issue peak is one wave64
 # instruction per 4 cycles per SIMD: 1024 SIMDs x 2.4 GHz / 4.
-ATTN_VALU_PER_TILE = {"v001_L4_ctx512_text64MiB": 1012}
+ATTN_VALU_PER_TILE = {"v001_L4_ctx512_text64MiB": 1006}
 PEAK_VALU_GINST = 1024 * 2.4 / 4 * 1e9 / 1e9
 
 WORKLOADS = {
