@@ -213,14 +213,17 @@ __device__ __forceinline__ int sra_rne32(int v, unsigned sh) {
 __device__ __forceinline__ int rne_shr(int v, int sh) { return (v + (1 << (sh - 1)) - 1 + ((v >> sh) & 1)) >> sh; }
 
 // RoPE rounding for |v| < 2^31: sra_rne32(v, 15) (m = 1, bb = 0) or
-// sra_rne32(sra_rne32(v, 15), 1) (m = 1/2, bb = B/2), B = 1.5 * 2^52 (ulp 1):
-// r1 = fma(v, 2^-15, B) is B + RNE(v / 2^15) exactly, and fma(r1, m, bb) is
-// B + r1's quotient times m rounded once (half to even, as the reference's
-// symmetric RNE); the low word is the result.
+// sra_rne32(sra_rne32(v, 15), 1) (m = 1/2, bb = B/2), B = 1.5 * 2^67, whose
+// ulp is 2^15: r1 = v + B is B + 2^15 RNE(v / 2^15) exactly (its mantissa
+// 1.5 * 2^52 + the quotient), and fma(r1, m, bb) is B + 2^15 times r1's
+// quotient times m rounded once (half to even, as the reference's symmetric
+// RNE); the low word is the result.  (An add with B held in scalar registers
+// where an FMA by 2^-15 would need B copied into vector registers each time.)
 __device__ __forceinline__ int rope_round(int v, double m, double bb) {
-    const double r1 = __builtin_fma((double)v, 0x1p-15, 6755399441055744.0);
+    const double r1 = (double)v + 221360928884514619392.0;  // 1.5 * 2^67
     return (int)(unsigned)__builtin_bit_cast(unsigned long long, __builtin_fma(r1, m, bb));
 }
+constexpr double ROPE_Q_BIAS = 110680464442257309696.0;  // bb of the query's second rounding: 0.75 * 2^67
 
 // primitives.rs:49-73
 __device__ __forceinline__ int sra_rne64(long long v, unsigned sh) {

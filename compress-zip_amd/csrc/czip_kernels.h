@@ -155,6 +155,7 @@ struct QkvTabArgs {
     int8_t* kc;              // [B, KH, T, 64]
     int8_t* vc;              // [B, KH, TP * 64] values transposed in blocks of 2^vl keys (vt_off)
     int vl = 4;
+    double inv_per_row = 0.0;  // 1 / (8 H + 24 NG), set by launch_qkv_table (the per-step kernel)
 };
 void launch_qkv_table(const QkvTabArgs& a, hipStream_t s);
 

@@ -215,7 +215,10 @@ __global__ __launch_bounds__(256) void k_qkv_table(QkvTabArgs a) {
     const int per_row = 8 * a.H + 24 * a.NG;
     const int idx = blockIdx.x * 256 + threadIdx.x;
     if (idx >= a.M * per_row) return;
-    const int row = idx / per_row, it = idx - row * per_row;
+    // idx / per_row from the host's 1 / per_row: the product is within 2^-21
+    // of the quotient, whose fraction is 0 or >= 1 / per_row >= 2^-12, so a
+    // 2^-13 bias truncates to it exactly (per_row < 2^12, idx < 2^31)
+    const int row = (int)__builtin_fma((double)idx, a.inv_per_row, 0x1p-13), it = idx - row * per_row;
     const int b = a.pos >= 0 ? row : row / a.T, p = a.pos >= 0 ? a.pos : row - b * a.T;
     const int8_t* t = a.tab + (size_t)a.tok[row] * a.qkv_n;
     if (it >= 8 * a.H + 8 * a.NG) {  // V: dims 4 q .. 4 q + 3 of head g, in blocks of 2^vl keys (vt_off)
@@ -229,7 +232,7 @@ __global__ __launch_bounds__(256) void k_qkv_table(QkvTabArgs a) {
     }
     const bool isq = it < 8 * a.H;
     // Q: >> 15 then NET_SHIFT = 1 (attention.rs:53-83); K: >> 15 (attention.rs:29-50)
-    const double rm = isq ? 0.5 : 1.0, rb = isq ? 3377699720527872.0 : 0.0;
+    const double rm = isq ? 0.5 : 1.0, rb = isq ? ROPE_Q_BIAS : 0.0;
     const int hd = isq ? it >> 3 : (it - 8 * a.H) >> 3, i0 = 4 * (it & 7);
     const int col = isq ? 64 * hd : a.d + 64 * hd;
     const unsigned xw = *(const unsigned*)(t + col + i0), yw = *(const unsigned*)(t + col + i0 + 32);
@@ -272,12 +275,18 @@ __global__ __launch_bounds__(256) void k_qkv_table_blk(QkvTabArgs a) {
     __syncthreads();
     // Q and K rotary groups: item = (row k, group i): group < 8H query, else key
     const int per_row = 8 * a.H + 8 * a.NG;
-    for (int idx = tid; idx < 16 * per_row; idx += 256) {
-        const int k = idx / per_row, it = idx - k * per_row;
+    // item idx = (row k, group it), advanced by 256 per pass: one division per thread
+    const int kstep = 256 / per_row, istep = 256 - kstep * per_row;
+    int k = tid / per_row, it = tid - k * per_row;
+    for (int idx = tid; idx < 16 * per_row; idx += 256, k += kstep, it += istep) {
+        if (it >= per_row) {
+            it -= per_row;
+            k++;
+        }
         const int8_t* t = a.tab + (size_t)tk[k] * a.qkv_n;
         const bool isq = it < 8 * a.H;
         // Q: >> 15 then NET_SHIFT = 1 (attention.rs:53-83); K: >> 15 (attention.rs:29-50)
-        const double rm = isq ? 0.5 : 1.0, rb = isq ? 3377699720527872.0 : 0.0;
+        const double rm = isq ? 0.5 : 1.0, rb = isq ? ROPE_Q_BIAS : 0.0;
         const int hd = isq ? it >> 3 : (it - 8 * a.H) >> 3, i0 = 4 * (it & 7);
         const int col = isq ? 64 * hd : a.d + 64 * hd;
         const unsigned xw = *(const unsigned*)(t + col + i0), yw = *(const unsigned*)(t + col + i0 + 32);
@@ -334,8 +343,12 @@ void launch_qkv_table(const QkvTabArgs& a, hipStream_t s) {
         hipLaunchKernelGGL(k_qkv_table_blk, dim3((unsigned)(nb * nkb)), dim3(256), 0, s, a);
         return;
     }
-    const long long n = (long long)a.M * (8 * a.H + 24 * a.NG);
-    hipLaunchKernelGGL(k_qkv_table, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+    const int per_row = 8 * a.H + 24 * a.NG;
+    const long long n = (long long)a.M * per_row;
+    // n < 2^31 (the caller takes the table path only then) and per_row <= 512 (d <= 1024)
+    QkvTabArgs g = a;
+    g.inv_per_row = 1.0 / per_row;
+    hipLaunchKernelGGL(k_qkv_table, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g);
 }
 
 // x += rmsnorm(y8, w1) (model.rs:429-434 / 463-468);
