@@ -2,7 +2,8 @@
 mirror (python/compress_zip of the reference tree), as an executor of the
 algorithm that is independent of this repository's C oracle and HIP path.
 
-Run in the build container only (the reference tree is not on the GPU box):
+Run where the reference tree is checked out (the GPU tests read only the
+fixtures it writes):
 
     python tests/golden/make_fixtures.py [--ref /root/reference/python] [--jobs 8]
 

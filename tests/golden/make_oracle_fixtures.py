@@ -1,7 +1,7 @@
 """Writes the oracle-coded fixtures of the two large random-init
 configurations, whose oracle runs take minutes (a 4096-token chunk of the
 d768 / 12-layer model codes at ~20 tokens/s on one core), so that the GPU
-tests compare against them instead of re-running the oracle on the GPU box:
+tests compare against them instead of re-running the oracle at test time:
 
   d512l8_ctx512.npz   d512 / 8 layers / 8 heads, 2 KV heads / F 2048 / V 1024
                       (reference KV semantics): 256 chunks of 512 Zipf(1.1)
