@@ -213,13 +213,15 @@ def test_unfused_ffn_path(gpu_shipped, shipped, monkeypatch, amd):
     assert np.array_equal(gm.decompress_chunks(ref, lens), toks)
 
 
-@pytest.mark.parametrize("chunk,n_chunks", [(512, 3), (96, 350)])
+@pytest.mark.parametrize("chunk,n_chunks", [(512, 3), (96, 350), (100, 340)])
 def test_fused_ffn_small_launches(amd, shipped, monkeypatch, chunk, n_chunks):
     """The fused FFN kernel (used from 2^19 rows) forced onto small launches:
-    1,536 rows, and 33,600 rows = 262.5 strips of 128 (a partial last strip,
+    1,536 rows; 33,600 rows = 262.5 strips of 128 (a partial last strip,
     more strips than the 256 workgroups, so some take a second strip with the
-    next strip's input prefetched); the compressed bytes against the oracle's,
-    and the decode, whose steps then run it too."""
+    next strip's input prefetched); 34,000 rows, whose 531.25 row blocks also
+    take the persistent LM head through several blocks per workgroup and a
+    partial last block; the compressed bytes against the oracle's, and the
+    decode, whose steps then run it too."""
     monkeypatch.setenv("CZIP_FFN_MIN_ROWS", "1")
     gm = amd.Model(amd.ModelWeights(MODEL_PATH))
     rng = np.random.default_rng(80 + chunk)
