@@ -40,6 +40,7 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void k_attention(AttnArgs a) {
     const int wrow0 = q0 + wave * 16;
     if (wrow0 >= len) return;  // no barrier follows
     AttnWaveLds& W = wl[wave];
+    attn_wave_init(W);
     const int D = a.H * 64;
     const int g = a.kv_mode == 1 ? (h * a.G) / a.H : 0;
     const double mscale = (double)a.score_mult[h] * (1.0 / 32768.0);

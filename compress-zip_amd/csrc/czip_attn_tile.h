@@ -45,8 +45,15 @@ constexpr int RS = 68;                // row stride (words) of the per-wave buff
 struct AttnWaveLds {
     unsigned buf[16][RS];    // per pass: the segment sums [row][dim]
     uint16_t ex[16][72];     // [row][key]: at a record key, the rescale factor ^ WB;
-                             // 144-byte rows: 16-byte stores of 16 rows hit 64 banks
+                             // 144-byte rows: 16-byte stores of 16 rows hit 64 banks;
+                             // slot 64: factor 0 (WB), read for a row with no split left
 };
+
+// Once per wave, before its first tile.
+__device__ __forceinline__ void attn_wave_init(AttnWaveLds& W) {
+    const int lane = threadIdx.x & 63;
+    if (lane < 16) W.ex[lane][64] = (uint16_t)WB;
+}
 
 __device__ __forceinline__ void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
 
@@ -88,7 +95,10 @@ __device__ __forceinline__ int attn_sink_m(int dot, double mscale) {
     return (int)score_u(dot, mscale * 0.25, score_bias_u(mscale));
 }
 
-// |a - b| of two u32 (v_sad_u32 with a zero accumulator)
+// |a - b| of two u32 (v_sad_u32 with a zero accumulator).  Inline asm is not
+// covered by the compiler's MFMA hazard checks (an asm write to a register
+// that an MFMA still in flight will write), so it is used only in the scan,
+// where every MFMA result has been read (checked in the kernels' assembly).
 __device__ __forceinline__ unsigned absdiff_u32(unsigned a, unsigned b) {
     unsigned r;
     asm("v_sad_u32 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
@@ -315,6 +325,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
     }
     const int nrow = __builtin_popcount(rlo) + __builtin_popcount(rhi);
     const unsigned seg = (unsigned)(__builtin_popcount(rlo & blo) + __builtin_popcount(rhi & bhi));
+    unsigned long long rsp = ((unsigned long long)rhi << 32) | rlo;  // the splits not yet passed
     // every key's factor, read at its split's pass
 #pragma unroll
     for (int h = 0; h < KPL / 8; h++) {
@@ -422,10 +433,22 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
         // record not yet passed; row r's is read by the combine from lane r
         unsigned erow = 0u;
         if (j >= 1) {
-            const int key = rlo ? __builtin_ctz(rlo) : 32 + __builtin_ctz(rhi | 0x80000000u);
-            erow = j <= nrow ? (unsigned)W.ex[row][key] ^ WB : 0u;
-            rhi = rlo ? rhi : rhi & (rhi - 1u);
-            rlo &= rlo - 1u;
+            if constexpr (NS == 1) {
+                // lowest split left: the low word's, else the high word's,
+                // else slot 64, which holds factor 0 (attn_wave_init) for a
+                // row with no split left
+                const unsigned lo = (unsigned)rsp, hi = (unsigned)(rsp >> 32);
+                const unsigned key = lo ? (unsigned)__builtin_ctzg(lo, 32) : 32u + (unsigned)__builtin_ctzg(hi, 32);
+                erow = (unsigned)W.ex[row][key] ^ WB;
+                rsp &= rsp - 1ull;
+            } else {
+                // the two-stream decode tile keeps the 32-bit form (the 64-bit
+                // one made its register allocation spill: 440 vs 415 ms)
+                const int key = rlo ? __builtin_ctz(rlo) : 32 + __builtin_ctz(rhi | 0x80000000u);
+                erow = j <= nrow ? (unsigned)W.ex[row][key] ^ WB : 0u;
+                rhi = rlo ? rhi : rhi & (rhi - 1u);
+                rlo &= rlo - 1u;
+            }
         }
         // 4a. S of this lane's row (lanes = rows): rescale at record j (a
         // factor of 65536 leaves S as it is), then add segment j

@@ -132,6 +132,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int G
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: streams, group and caches in SGPRs
     const int row = lane & 15, grp = lane >> 4;
     for (int i = tid; i < ETB_PAD / 8; i += 256) ((uint4*)etb)[i] = ((const uint4*)a.etab)[i];
+    attn_wave_init(wl[wave]);
     __syncthreads();
     const int item = (int)blockIdx.x * 4 + wave;
     const int sp = item / a.KH, g = item % a.KH;
