@@ -35,7 +35,7 @@ TRAFFIC_WORKLOADS = ("v001_L4_ctx512_text64MiB",)
 # SQ_INSTS_VALU - SQ_INSTS_VALU_MFMA_I8 on the same workload
 # (profiles/counters_compress_v001_ctx512_text8Mtok.md); the VALU issue peak is one wave64
 # instruction per 4 cycles per SIMD: 1024 SIMDs x 2.4 GHz / 4.
-ATTN_VALU_PER_TILE = {"v001_L4_ctx512_text64MiB": 1006}
+ATTN_VALU_PER_TILE = {"v001_L4_ctx512_text64MiB": 990}
 PEAK_VALU_GINST = 1024 * 2.4 / 4 * 1e9 / 1e9
 
 WORKLOADS = {
