@@ -541,7 +541,7 @@ RowBufs row_bufs(const czip_ctx* c, const czip_job* j, int64_t r0 = 0, int ws_pa
                    j->rn_ws ? j->rn_ws + wb / 4 * (size_t)ws_part : nullptr, wb};
 }
 
-void post_attention(czip_ctx* c, const RowBufs& r, int l, int M, hipStream_t s) {
+void post_attention(czip_ctx* c, const RowBufs& r, int l, int M, hipStream_t s, bool beside_lanes = false) {
     const int d = c->cfg.d_model, F = c->cfg.d_ff;
     const DevLayer& L = c->layers[(size_t)l];
     const bool last = l + 1 == c->cfg.n_layers;
@@ -562,9 +562,11 @@ void post_attention(czip_ctx* c, const RowBufs& r, int l, int M, hipStream_t s) 
         { Timed t(c, "row_norm"); launch_resid_norm(r.x, r.y8, L.ffn_norm, L.post_attn_norm, M, d, r.xn, s); }
     }
     // the fused FFN walks 128-row strips with one workgroup per CU: it pays
-    // off for prefill sub-batches, while a decode step's few thousand rows
-    // balance better over the separate kernels' 64-row blocks
-    if (c->ffn_fused && M >= c->ffn_min_rows) {
+    // off for prefill sub-batches, while a decode step's rows alone balance
+    // better over the separate kernels' 64-row blocks; beside other decode
+    // lanes (which fill its last round of strips) its one launch per layer
+    // instead of two is the faster choice again
+    if (c->ffn_fused && (M >= c->ffn_min_rows || beside_lanes)) {
         GemmArgs u{}, dn{};  // requantization parameters of the two products
         u.K = d; set_requant(u, L.up_mult, L.up_shift);
         dn.K = F; set_requant(dn, L.down_mult, L.down_shift);
@@ -1097,7 +1099,7 @@ static czip_status run_decompress(czip_job* j) {
                     a.G = c->cfg.n_kv_heads; a.KH = c->KH; a.kv_mode = c->cfg.kv_mode; a.coef = 378194u;
                     a.general = L.attn_general;
                     { Timed t(c, "attn_decode"); launch_attn_decode(a, M, p, s); }
-                    post_attention(c, Ln.r, l, M, s);
+                    post_attention(c, Ln.r, l, M, s, nl > 1);
                 }
                 if (c->head_fused) {
                     HeadDecArgs h{};
