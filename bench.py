@@ -24,6 +24,9 @@ import numpy as np  # noqa: E402
 PEAK_INT8_TOPS = 5000.0     # TOP/s
 PEAK_HBM_GBS = 8000.0       # GB/s
 
+# The commit the two profile-derived constants below were measured at (they go
+# stale when the kernels change; the bench line carries this name with them).
+PROFILED_AT = "f52d556"
 # HBM bytes per token (read + write) of each kernel on the text workload, from
 # two rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0: the factors a
 # plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text.md
@@ -141,6 +144,23 @@ def cpu_baseline(model_path, tokens, chunk, budget_s=15.0, kv_mode=0, extra_chun
     return rec, coded
 
 
+def ceilings():
+    """The measured ceilings beside the published peaks: a streaming copy of
+    1 GiB (read + write bytes over time) and dense int8 MFMA chains with no
+    memory traffic (8 waves per SIMD), from libczip_ceiling.so."""
+    import ctypes as C
+    from czip_amd import build as b
+    L = C.CDLL(b.CEILING_LIB_PATH)
+    L.czc_copy_gbs.argtypes = [C.c_size_t, C.c_int, C.POINTER(C.c_double)]
+    L.czc_mfma_i8_tops.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double)]
+    gbs, tops = C.c_double(), C.c_double()
+    if L.czc_copy_gbs(1 << 30, 10, C.byref(gbs)) or L.czc_mfma_i8_tops(20000, 8, C.byref(tops)):
+        raise SystemExit("ceiling probes failed")
+    return {"hbm_copy_gbs": round(gbs.value, 1), "int8_mfma_tops": round(tops.value, 1),
+            "copy": "1 GiB device-to-device copy kernel, 16-byte loads/stores, 10 timed passes",
+            "mfma": "v_mfma_i32_16x16x64_i8, 8 independent chains per wave, 8 waves per SIMD, no memory traffic"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -183,6 +203,8 @@ def main():
     n = int(tokens.size)
     log(f"workload {args.workload}: {n} tokens, chunk {chunk}")
     model = czip_amd.Model(weights, device=0)
+    ceil = ceilings()
+    log(f"ceilings: copy {ceil['hbm_copy_gbs']:.0f} GB/s, int8 MFMA {ceil['int8_mfma_tops']:.0f} TOP/s")
     t_plan = time.perf_counter()
     job = model.compress_plan(tokens, chunk)  # device buffers + host-to-device copy of the tokens
     plan_ms = (time.perf_counter() - t_plan) * 1000.0
@@ -256,7 +278,13 @@ def main():
     if args.workload in TRAFFIC_WORKLOADS and roof["kernel"] in TRAFFIC_B_PER_TOKEN:
         per_launch_tokens = n / (kernels[dom]["launches"] / prof_steps)
         roof["traffic"] = round(TRAFFIC_B_PER_TOKEN[roof["kernel"]] * per_launch_tokens)
-        roof["traffic_source"] = "rocprofv3 FETCH_SIZE/WRITE_SIZE per token x tokens per launch"
+        roof["traffic_source"] = (f"rocprofv3 FETCH_SIZE/WRITE_SIZE per token (profiled at {PROFILED_AT}) "
+                                  f"x tokens per launch")
+    if "valu" in roof:
+        roof["valu"]["profiled_at"] = PROFILED_AT
+    # the same rate against the measured ceiling of its resource
+    roof["frac_of_measured"] = round(roof["achieved"] / (ceil["int8_mfma_tops"] if roof["bound"] == "mfma"
+                                                         else ceil["hbm_copy_gbs"]), 5)
 
     # decompress leg: the chunks just coded, decoded back on the device as
     # concurrent streams (one token per stream per step), checked for identity
@@ -302,7 +330,7 @@ def main():
             gbs = alg / (dk["attn_decode"]["ms"] / 1000.0) / 1e9
             dec["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                                "frac": round(gbs / PEAK_HBM_GBS, 4), "kernel": "attn_decode",
-                               "algorithmic_bytes": alg}
+                               "algorithmic_bytes": alg, "frac_of_measured": round(gbs / ceil["hbm_copy_gbs"], 4)}
 
     cpu = None
     parity = None
@@ -331,6 +359,9 @@ def main():
         "e2e": e2e,
         "decompress": dec,
         "gemm_int8_tops": round(gemm_tops, 2),
+        "gemm_int8_frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
+        "gemm_int8_frac_of_measured": round(gemm_tops / ceil["int8_mfma_tops"], 4),
+        "ceilings": ceil,
         "coded_bytes": coded,
         "kernels": {k: {"avg_ms": round(v["avg_ms"], 4), "ms_per_step": round(v["ms_per_step"], 3),
                         "launches_per_step": v["launches"] // prof_steps} for k, v in kernels.items()},

@@ -26,6 +26,7 @@ constexpr int FFN_MIN_ROWS = 1 << 19;  // rows from which a layer's FFN runs as 
 // a compress sub-batch, or a decode group's caches; 32 GB of the 288 GB
 // halves the shipped model's 64 MiB-text job to 7 sub-batches (+0.5% against 16)
 constexpr double SCRATCH_GB_DEFAULT = 32.0;
+constexpr int DEC_LANES_MAX = 4;  // most HIP streams a decode group is split over
 // V^T block exponent of the decode caches (vt_off): a step appends one key, whose 64 value
 // bytes span 256 bytes with 4-key blocks (1 KB with the prefill caches' 16-key blocks); the
 // decode attention reads this layout
@@ -89,6 +90,12 @@ struct czip_ctx {
     bool head_fused = false;  // LM head fused with the coder interval stage / decode step (head_cdf_supported(vocab))
     bool ffn_fused = false;   // up + ReGLU + down + norms in one kernel (ffn_supported(d_model, d_ff))
     int64_t ffn_min_rows = FFN_MIN_ROWS;  // rows from which it is used (CZIP_FFN_MIN_ROWS)
+    // switches read from the environment once, at czip_create
+    bool gemm_tiled = false;      // CZIP_GEMM_TILED: tiled GEMM kernels only
+    bool qkv_gemm = false;        // CZIP_QKV_GEMM: layer 0's QKV by the GEMM, not the per-token table
+    double scratch_gb = 0;        // CZIP_SCRATCH_GB: a job's scratch budget
+    int64_t decode_streams = 0;   // CZIP_DECODE_STREAMS: most streams per decode group (0: no cap)
+    int decode_lanes = 0;         // CZIP_DECODE_LANES: lanes per decode group (0: by group size)
     std::vector<void*> allocs;
     int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr, *head_wf = nullptr;
     int8_t* embed_xn = nullptr;  // rmsnorm(embed[v], layer 0's attn_norm) for every token v
@@ -117,6 +124,7 @@ struct czip_job {
     int64_t n_tokens = 0, nchunks = 0;
     int T = 0, BC = 0;
     int64_t slot = 0;
+    bool ran = false;  // the last czip_job_run succeeded: the outputs may be fetched
     std::vector<void*> allocs;
     uint32_t* tok = nullptr;
     uint8_t* out = nullptr;
@@ -142,6 +150,7 @@ struct czip_job {
     // step-wise decode session
     uint32_t *d_val = nullptr, *d_out = nullptr;
     std::vector<int32_t> h_lens;
+    std::vector<int32_t> h_done;  // per stream: the highest position whose K/V are cached since it last began at 0 (-1: none)
 };
 
 namespace {
@@ -235,6 +244,16 @@ void resolve_events(czip_ctx* c) {
         c->event_pool.push_back(p.b);
     }
     c->pending.clear();
+}
+
+// the GEMM launches with the context's kernel switch
+void gemm(const czip_ctx* c, GemmArgs g, int epi, hipStream_t s) {
+    g.tiled = c->gemm_tiled ? 1 : 0;
+    launch_gemm(g, epi, s);
+}
+void gemm_rn(const czip_ctx* c, RowGemmArgs a, hipStream_t s) {
+    a.tiled = c->gemm_tiled ? 1 : 0;
+    launch_gemm_rn(a, s);
 }
 
 czip_status check_config(czip_ctx* c, const czip_model_desc& w) {
@@ -358,6 +377,15 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
     c->head_fused = head_cdf_supported(w->vocab) && w->coef_q24 < (1u << 23) && getenv("CZIP_UNFUSED_HEAD") == nullptr;
     c->ffn_fused = c->rn_fused && ffn_supported(w->d_model, w->d_ff) && getenv("CZIP_UNFUSED_FFN") == nullptr;
     if (const char* e = getenv("CZIP_FFN_MIN_ROWS")) c->ffn_min_rows = std::max(1ll, atoll(e));
+    c->gemm_tiled = getenv("CZIP_GEMM_TILED") != nullptr;
+    c->qkv_gemm = getenv("CZIP_QKV_GEMM") != nullptr;
+    c->scratch_gb = SCRATCH_GB_DEFAULT;
+    if (const char* e = getenv("CZIP_SCRATCH_GB")) c->scratch_gb = atof(e);
+    if (const char* e = getenv("CZIP_DECODE_STREAMS")) c->decode_streams = std::max(1ll, atoll(e));
+    if (const char* e = getenv("CZIP_DECODE_LANES")) {
+        const int n = atoi(e);
+        if (n >= 1 && n <= DEC_LANES_MAX) c->decode_lanes = n;
+    }
     czip_ctx* C = c.get();
 #define UP(dst, src, n) if ((rc = upload(C, &dst, src, n))) return rc;
     UP(c->embed, w->embed, V * d)
@@ -427,7 +455,7 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
         GemmArgs g{};
         g.A = c->embed_xn; g.W = L0.qkv_w; g.M = (int)V; g.N = L0.qkv_n; g.K = (int)d;
         g.out8 = c->qkv_tab; g.ldo = L0.qkv_n; set_requant(g, L0.qkv_mult, L0.qkv_shift);
-        launch_gemm(g, EPI_REQ, c->stream);
+        gemm(C, g, EPI_REQ, c->stream);
         HIPCHECK(C, hipGetLastError());
         HIPCHECK(C, hipStreamSynchronize(c->stream));
     }
@@ -510,8 +538,7 @@ czip_status alloc_scratch(czip_ctx* c, czip_job* j, int BC, int T, bool logits =
 }
 
 int pick_batch_chunks(const czip_ctx* c, int64_t nchunks, int T, bool logits = true) {
-    double gb = SCRATCH_GB_DEFAULT;
-    if (const char* s = getenv("CZIP_SCRATCH_GB")) gb = atof(s);
+    const double gb = c->scratch_gb;
     double per_chunk = (double)row_bytes(c, logits) * T;
     int64_t bc = (int64_t)(gb * 1e9 / per_chunk);
     bc = std::max<int64_t>(1, std::min<int64_t>(bc, nchunks));
@@ -553,12 +580,12 @@ void post_attention(czip_ctx* c, const RowBufs& r, int l, int M, hipStream_t s, 
         o.w1 = L.ffn_norm; o.w2 = L.post_attn_norm;
         o.x_in = l == 0 ? nullptr : r.x; o.tok = r.inp; o.embed = c->embed;
         o.x_out = r.x; o.xn = r.xn; o.ws = r.rn_ws; o.ws_bytes = r.rn_ws_bytes;
-        { Timed t(c, "gemm_o_norm"); launch_gemm_rn(o, s); }
+        { Timed t(c, "gemm_o_norm"); gemm_rn(c, o, s); }
     } else {
         GemmArgs o{};
         o.A = r.attn; o.W = L.out_w; o.M = M; o.N = d; o.K = d; o.out8 = r.y8; o.ldo = d;
         set_requant(o, L.out_mult, L.out_shift);
-        { Timed t(c, "gemm_o"); launch_gemm(o, EPI_REQ, s); }
+        { Timed t(c, "gemm_o"); gemm(c, o, EPI_REQ, s); }
         { Timed t(c, "row_norm"); launch_resid_norm(r.x, r.y8, L.ffn_norm, L.post_attn_norm, M, d, r.xn, s); }
     }
     // the fused FFN walks 128-row strips with one workgroup per CU: it pays
@@ -582,19 +609,19 @@ void post_attention(czip_ctx* c, const RowBufs& r, int l, int M, hipStream_t s, 
     GemmArgs u{};
     u.A = r.xn; u.W = L.up_w; u.M = M; u.N = 2 * F; u.K = d; u.out8 = r.r8; u.ldo = F;
     set_requant(u, L.up_mult, L.up_shift);
-    { Timed t(c, "gemm_up"); launch_gemm(u, EPI_REGLU, s); }
+    { Timed t(c, "gemm_up"); gemm(c, u, EPI_REGLU, s); }
     if (c->rn_fused) {
         RowGemmArgs dn{};
         dn.A = r.r8; dn.W = L.down_w; dn.Wf = L.down_wf; dn.M = M; dn.K = F; dn.d = d;
         set_requant(dn, L.down_mult, L.down_shift);
         dn.w1 = L.post_ffn_norm; dn.w2 = next;
         dn.x_in = r.x; dn.x_out = last ? nullptr : r.x; dn.xn = r.xn; dn.ws = r.rn_ws; dn.ws_bytes = r.rn_ws_bytes;
-        { Timed t(c, "gemm_down_norm"); launch_gemm_rn(dn, s); }
+        { Timed t(c, "gemm_down_norm"); gemm_rn(c, dn, s); }
     } else {
         GemmArgs dn{};
         dn.A = r.r8; dn.W = L.down_w; dn.M = M; dn.N = d; dn.K = F; dn.out8 = r.y8; dn.ldo = d;
         set_requant(dn, L.down_mult, L.down_shift);
-        { Timed t(c, "gemm_down"); launch_gemm(dn, EPI_REQ, s); }
+        { Timed t(c, "gemm_down"); gemm(c, dn, EPI_REQ, s); }
         { Timed t(c, "row_norm"); launch_resid_norm(r.x, r.y8, L.post_ffn_norm, next, M, d, r.xn, s); }
     }
 }
@@ -606,7 +633,7 @@ void layer0_qkv(czip_ctx* c, GemmArgs& g, const uint32_t* tok, hipStream_t s) {
     const DevLayer& L = c->layers[0];
     const int NG = c->cfg.kv_mode == CZIP_KV_GQA ? c->cfg.n_kv_heads : 1;
     const long long items = (long long)g.M * (8 * c->cfg.n_heads + 24 * NG);
-    if (getenv("CZIP_QKV_GEMM") == nullptr && items < (1ll << 31)) {
+    if (!c->qkv_gemm && items < (1ll << 31)) {
         QkvTabArgs q{};
         q.tab = c->qkv_tab; q.tok = tok; q.M = g.M; q.T = g.T; q.TP = g.TP; q.pos = g.pos; q.vl = g.vl;
         q.H = c->cfg.n_heads; q.NG = NG; q.KH = c->KH; q.d = c->cfg.d_model; q.qkv_n = L.qkv_n;
@@ -617,7 +644,7 @@ void layer0_qkv(czip_ctx* c, GemmArgs& g, const uint32_t* tok, hipStream_t s) {
     }
     g.A = c->embed_xn; g.a_rows = tok; g.a_nrows = c->cfg.vocab;
     Timed t(c, "gemm_qkv");
-    launch_gemm(g, EPI_QKV, s);
+    gemm(c, g, EPI_QKV, s);
 }
 
 // Run every layer on rows [0, nb*T) whose inputs are j->inp / j->lens; leaves
@@ -642,7 +669,7 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T, bool head = t
             layer0_qkv(c, g, j->inp, s);
         } else {
             Timed t(c, "gemm_qkv");
-            launch_gemm(g, EPI_QKV, s);
+            gemm(c, g, EPI_QKV, s);
         }
         AttnArgs a{};
         a.q = j->q8; a.kc = j->kc; a.vc = j->vc; a.TP = pad64(T); a.lens = j->lens; a.score_mult = L.score_mult;
@@ -656,7 +683,7 @@ czip_status forward_batch(czip_ctx* c, czip_job* j, int nb, int T, bool head = t
         GemmArgs h{};
         h.A = j->xn; h.W = c->head_w; h.M = M; h.N = V; h.K = d; h.out32 = j->logits; h.ldo = V;
         Timed t(c, "gemm_head");
-        launch_gemm(h, EPI_RAW, s);
+        gemm(c, h, EPI_RAW, s);
     }
     return CZIP_OK;
 }
@@ -803,6 +830,10 @@ extern "C" czip_status czip_compress_plan(czip_ctx* c, const uint32_t* tokens, i
     if ((rc = dalloc(c, j->allocs, &j->tok, (size_t)std::max<int64_t>(n, 1)))) { free_job_mem(j.get()); return rc; }
     if ((rc = dalloc(c, j->allocs, &j->out, (size_t)(nch * j->slot)))) { free_job_mem(j.get()); return rc; }
     if ((rc = dalloc(c, j->allocs, &j->out_lens, (size_t)nch))) { free_job_mem(j.get()); return rc; }
+    if (nch > 0 && hipMemset(j->out_lens, 0, (size_t)nch * 4) != hipSuccess) {
+        free_job_mem(j.get());
+        return fail(c, CZIP_E_HIP, "hipMemset of the chunk lengths");
+    }
     if ((rc = dalloc(c, j->allocs, &j->err, 1))) { free_job_mem(j.get()); return rc; }
     // coder intervals and lengths of every chunk, so one encoder launch covers all chunks
     if ((rc = dalloc(c, j->allocs, &j->lohi_all, (size_t)(nch * chunk * 2)))) { free_job_mem(j.get()); return rc; }
@@ -860,19 +891,27 @@ static czip_status run_decompress(czip_job* j);
 
 extern "C" czip_status czip_job_run(czip_job* j) {
     if (!j) return CZIP_E_ARG;
+    j->ran = false;
     HIPCHECK(j->ctx, hipSetDevice(j->ctx->device));
-    if (j->kind == 0) return run_compress(j);
-    if (j->kind == 1) return run_decompress(j);
-    return fail(j->ctx, CZIP_E_ARG, "unknown job kind");
+    czip_status rc;
+    if (j->kind == 0) rc = run_compress(j);
+    else if (j->kind == 1) rc = run_decompress(j);
+    else return fail(j->ctx, CZIP_E_ARG, "unknown job kind");
+    j->ran = rc == CZIP_OK;
+    return rc;
 }
 
 extern "C" czip_status czip_compress_fetch(czip_job* j, uint8_t* out, int64_t slot, int32_t* lens) {
     if (!j || j->kind != 0 || !lens || (j->nchunks > 0 && !out)) return CZIP_E_ARG;
     czip_ctx* c = j->ctx;
     if (j->nchunks == 0) return CZIP_OK;
+    if (!j->ran) return fail(c, CZIP_E_ARG, "fetch before a successful czip_job_run");
+    HIPCHECK(c, hipSetDevice(c->device));
     HIPCHECK(c, hipMemcpy(lens, j->out_lens, (size_t)j->nchunks * 4, hipMemcpyDeviceToHost));
-    for (int64_t i = 0; i < j->nchunks; i++)
+    for (int64_t i = 0; i < j->nchunks; i++) {
+        if (lens[i] < 0 || lens[i] > j->slot) return fail(c, CZIP_E_OVERFLOW, "coded chunk length outside its slot");
         if (lens[i] > slot) return fail(c, CZIP_E_OVERFLOW, "caller slot smaller than a coded chunk");
+    }
     if (slot == j->slot) {
         HIPCHECK(c, hipMemcpy(out, j->out, (size_t)(j->nchunks * j->slot), hipMemcpyDeviceToHost));
     } else {
@@ -887,11 +926,17 @@ extern "C" czip_status czip_compress_fetch_packed(czip_job* j, uint8_t* out, int
     czip_ctx* c = j->ctx;
     offs[0] = 0;
     if (j->nchunks == 0) return CZIP_OK;
+    if (!j->ran) return fail(c, CZIP_E_ARG, "fetch before a successful czip_job_run");
     const size_t n = (size_t)j->nchunks;
     std::vector<int32_t> lens(n);
     HIPCHECK(c, hipSetDevice(c->device));
     HIPCHECK(c, hipMemcpy(lens.data(), j->out_lens, n * 4, hipMemcpyDeviceToHost));
-    for (size_t i = 0; i < n; i++) offs[i + 1] = offs[i] + lens[i];
+    // the packing kernel reads lens[i] bytes of slot i: every length must lie
+    // in its slot before it is launched
+    for (size_t i = 0; i < n; i++) {
+        if (lens[i] < 0 || lens[i] > j->slot) return fail(c, CZIP_E_OVERFLOW, "coded chunk length outside its slot");
+        offs[i + 1] = offs[i] + lens[i];
+    }
     if (!out) return CZIP_OK;
     if (offs[n] > cap) return fail(c, CZIP_E_OVERFLOW, "output smaller than the coded bytes");
     std::vector<void*> tmp;
@@ -945,11 +990,10 @@ extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t* data, co
     j->total_tokens = total_tokens;
     j->h_ntok.assign(ntoks, ntoks + nchunks);
     const size_t d = (size_t)c->cfg.d_model, L = (size_t)c->cfg.n_layers;
-    double gb = SCRATCH_GB_DEFAULT;
-    if (const char* s = getenv("CZIP_SCRATCH_GB")) gb = atof(s);
+    const double gb = c->scratch_gb;
     const double per_stream = (double)row_bytes(c, !c->head_fused) + 2.0 * L * (double)c->KH * pad64(Tcap) * 64 + 64;
     int64_t S = (int64_t)(gb * 1e9 / per_stream);
-    if (const char* s = getenv("CZIP_DECODE_STREAMS")) S = std::min<int64_t>(S, atoll(s));
+    if (c->decode_streams > 0) S = std::min<int64_t>(S, c->decode_streams);
     S = std::min<int64_t>(S, INT32_MAX / (int64_t)d);  // decode row offsets are 32-bit
     S = std::max<int64_t>(1, std::min<int64_t>(S, std::max(nchunks, 1)));
     j->S = (int)S;
@@ -997,16 +1041,12 @@ extern "C" czip_status czip_decompress_plan(czip_ctx* c, const uint8_t* data, co
 // four lose to their smaller launches).  Not while per-kernel events are
 // recorded (they time one stream), nor for groups whose lanes would be small;
 // CZIP_DECODE_LANES=n (1..4) sets the number for every group.
-constexpr int DEC_LANES_MAX = 4;
 constexpr int DEC_LANE_MIN_STREAMS = 16384;
 constexpr int DEC_LANES_DEFAULT = 2;
 
 static int decode_lanes(const czip_ctx* c, int S) {
     if (c->profiling) return 1;
-    if (const char* e = getenv("CZIP_DECODE_LANES")) {
-        const int n = atoi(e);
-        if (n >= 1 && n <= DEC_LANES_MAX) return std::min(n, S);
-    }
+    if (c->decode_lanes > 0) return std::min(c->decode_lanes, S);
     return std::max(1, std::min(DEC_LANES_DEFAULT, S / DEC_LANE_MIN_STREAMS));
 }
 
@@ -1091,7 +1131,7 @@ static czip_status run_decompress(czip_job* j) {
                         layer0_qkv(c, g, Ln.r.inp, s);
                     } else {
                         Timed t(c, "gemm_qkv");
-                        launch_gemm(g, EPI_QKV, s);
+                        gemm(c, g, EPI_QKV, s);
                     }
                     AttnArgs a{};
                     a.q = Ln.r.q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = Ln.ds.ntok; a.score_mult = L.score_mult;
@@ -1111,7 +1151,7 @@ static czip_status run_decompress(czip_job* j) {
                     GemmArgs hd{};
                     hd.A = Ln.r.xn; hd.W = c->head_w; hd.M = M; hd.N = V; hd.K = d;
                     hd.out32 = j->logits + (size_t)Ln.r0 * V; hd.ldo = V;
-                    { Timed t(c, "gemm_head"); launch_gemm(hd, EPI_RAW, s); }
+                    { Timed t(c, "gemm_head"); gemm(c, hd, EPI_RAW, s); }
                     {
                         Timed t(c, "cdf_decode");
                         launch_cdf_decode(hd.out32, M, V, c->lut, c->cfg.coef_q24, c->cfg.target_total, p, Ln.st, Ln.ds, s);
@@ -1134,6 +1174,8 @@ extern "C" czip_status czip_decompress_fetch(czip_job* j, uint32_t* tokens_out, 
     if (!j || j->kind != 1 || (j->total_tokens > 0 && !tokens_out)) return CZIP_E_ARG;
     czip_ctx* c = j->ctx;
     if (j->total_tokens == 0) return CZIP_OK;
+    if (!j->ran) return fail(c, CZIP_E_ARG, "fetch before a successful czip_job_run");
+    HIPCHECK(c, hipSetDevice(c->device));
     if (!tok_offs) {
         HIPCHECK(c, hipMemcpy(tokens_out, j->d_tokens, (size_t)j->total_tokens * 4, hipMemcpyDeviceToHost));
         return CZIP_OK;
@@ -1199,6 +1241,7 @@ extern "C" czip_status czip_decode_begin(czip_ctx* c, int32_t S, int32_t T) {
     }
     j->rn_ws_bytes = gemm_rn_ws_bytes(S, (int)d);
     j->h_lens.assign((size_t)S, -1);
+    j->h_done.assign((size_t)S, -1);
     c->dec = j.release();
     return CZIP_OK;
 }
@@ -1223,9 +1266,16 @@ extern "C" czip_status czip_decode_step(czip_ctx* c, const uint32_t* tok_in, con
         return CZIP_OK;
     }
     if (p >= j->T) return fail(c, CZIP_E_RANGE, "position past the session's T (lut.rs:169-177)");
+    for (int i = 0; i < S; i++) {
+        if (pos[i] < 0) continue;
+        if (tok_in[i] >= (uint32_t)V) return fail(c, CZIP_E_TOKEN, "token id >= vocab at stream " + std::to_string(i));
+        // attention at p reads the stream's cached keys 0..p-1
+        if (p > 0 && j->h_done[(size_t)i] < p - 1)
+            return fail(c, CZIP_E_ARG, "stream " + std::to_string(i) + " is active at position " + std::to_string(p) +
+                                           " but its positions before it were never decoded");
+    }
     for (int i = 0; i < S; i++)
-        if (pos[i] >= 0 && tok_in[i] >= (uint32_t)V)
-            return fail(c, CZIP_E_TOKEN, "token id >= vocab at stream " + std::to_string(i));
+        if (pos[i] >= 0) j->h_done[(size_t)i] = p == 0 ? 0 : std::max(j->h_done[(size_t)i], p);
     HIPCHECK(c, hipSetDevice(c->device));
     hipStream_t s = c->stream;
     // inactive streams (pos -1) attend to nothing and read token 0; their rows are zeroed below
@@ -1256,7 +1306,7 @@ extern "C" czip_status czip_decode_step(czip_ctx* c, const uint32_t* tok_in, con
             layer0_qkv(c, g, j->inp, s);
         } else {
             Timed t(c, "gemm_qkv");
-            launch_gemm(g, EPI_QKV, s);
+            gemm(c, g, EPI_QKV, s);
         }
         AttnArgs a{};
         a.q = j->q8; a.kc = kc; a.vc = vc; a.TP = TP; a.lens = j->d_ntok; a.score_mult = L.score_mult;
@@ -1269,7 +1319,7 @@ extern "C" czip_status czip_decode_step(czip_ctx* c, const uint32_t* tok_in, con
     {
         GemmArgs hd{};
         hd.A = j->xn; hd.W = c->head_w; hd.M = S; hd.N = V; hd.K = d; hd.out32 = j->logits; hd.ldo = V;
-        { Timed t(c, "gemm_head"); launch_gemm(hd, EPI_RAW, s); }
+        { Timed t(c, "gemm_head"); gemm(c, hd, EPI_RAW, s); }
         Timed t(c, "cdf");
         launch_cdf(j->logits, S, V, value_or_null ? j->d_val : nullptr, nullptr, 1, c->lut, c->cfg.coef_q24,
                    c->cfg.target_total, value_or_null ? 2 : 1, j->d_out, 0, s);
@@ -1351,6 +1401,10 @@ extern "C" czip_status czip_prefill_cdf_noalloc(czip_ctx* c, const uint32_t* d_t
                     "B * T = " + std::to_string((long long)B * T) + " rows need " + std::to_string(size.off) +
                         " bytes of scratch; the no-alloc entry point holds " + std::to_string(NOALLOC_SCRATCH_BYTES));
     HIPCHECK(c, hipSetDevice(c->device));
+    // the context's stream does not wait for the caller's streams (it is a
+    // non-blocking stream): finish everything queued on the device, so inputs
+    // that the caller produced asynchronously have landed before they are read
+    HIPCHECK(c, hipDeviceSynchronize());
     hipStream_t s = c->stream;
     Carve cv{c->noalloc};
     int32_t* err = carve_prefill(c, &j, cv, B, T);

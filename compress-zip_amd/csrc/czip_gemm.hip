@@ -551,8 +551,7 @@ static void launch_ws(const GemmArgs& a, hipStream_t s) {
 
 template <int EPI>
 static bool try_ws(const GemmArgs& a, hipStream_t s) {
-    const bool off = getenv("CZIP_GEMM_TILED") != nullptr;  // read per launch (tests switch it)
-    if (off || a.N % 64 != 0 || (long long)a.N * a.K >= (1ll << 31) || a.M <= 0) return false;
+    if (a.tiled || a.N % 64 != 0 || (long long)a.N * a.K >= (1ll << 31) || a.M <= 0) return false;
     // 32-bit buffer offsets: the output rows, and the cache span of one strip
     if (64ll * a.ldo * (EPI == EPI_RAW ? 4 : 1) >= (1ll << 31)) return false;
     if (EPI == EPI_QKV && ((long long)a.KH * a.TP * 64 >= (1ll << 24) || a.T > a.TP)) return false;
@@ -900,8 +899,7 @@ static void launch_rn(const RowGemmArgs& a, hipStream_t s) {
 // d = 64 h columns over NW waves of CT 16-wide tiles: 8 waves where h is even
 // (few accumulators per wave, many waves to hide the W stream's latency)
 void launch_gemm_rn(const RowGemmArgs& a, hipStream_t s) {
-    const bool tiled = getenv("CZIP_GEMM_TILED") != nullptr;
-    if (!tiled && a.d == 384 && a.M > 0 && (long long)a.M * a.K < (1ll << 40)) {
+    if (!a.tiled && a.d == 384 && a.M > 0 && (long long)a.M * a.K < (1ll << 40)) {
         if (a.K == 384) { launch_rn_ws<8, 3, 6>(a, s); return; }
         if (a.K == 512) { launch_rn_ws<8, 3, 8>(a, s); return; }
     }

@@ -35,6 +35,7 @@ struct GemmArgs {
     int pos;          // >= 0: every row is at this position and row = chunk (decode step)
     const int16_t* rcos;
     const int16_t* rsin;
+    int tiled;        // 1: the tiled kernel only (no W-stationary one; a per-context test switch)
 };
 
 // The attention's exp table by table step t (exp_q16, lut.rs:213-235):
@@ -95,6 +96,7 @@ struct RowGemmArgs {
     int8_t* xn;            // [M, d]
     int32_t* ws;           // optional workspace of ws_bytes for the split-K path (few rows)
     size_t ws_bytes;
+    int tiled;             // 1: the tiled row kernel only (no W-stationary one; a per-context test switch)
 };
 bool gemm_rn_supported(int d);
 // bytes of workspace the split-K row GEMM wants for M rows of width d (0: M is large enough without)

@@ -2,7 +2,9 @@
 
 Every HIP translation unit is compiled with hipcc for gfx950 only, with the
 packed-FP32 instructions disabled, then linked into one shared library that
-exports the C-ABI of include/czip_hip.h.
+exports the C-ABI of include/czip_hip.h.  The benchmark's ceiling probes (a
+copy kernel and an int8 MFMA loop) go into a library of their own,
+libczip_ceiling.so.
 """
 from __future__ import annotations
 
@@ -15,6 +17,8 @@ ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(ROOT, "csrc")
 BUILD_DIR = os.path.join(ROOT, "_build")
 LIB_PATH = os.path.join(ROOT, "libczip_hip.so")
+CEILING_SOURCE = "czip_ceiling.hip"
+CEILING_LIB_PATH = os.path.join(ROOT, "libczip_ceiling.so")
 
 SOURCES = ["czip_rows.hip", "czip_gemm.hip", "czip_head.hip", "czip_attention.hip", "czip_decode.hip", "czip_ffn.hip",
            "czip_api.cpp",
@@ -34,18 +38,23 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD_DIR, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB_PATH + ".tmp"
+def _link(objs, path: str):
+    tmp = path + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, path)
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=len(SOURCES) + 1) as ex:
+        objs = list(ex.map(_compile, SOURCES + [CEILING_SOURCE]))
+    _link(objs[:-1], LIB_PATH)
+    _link(objs[-1:], CEILING_LIB_PATH)
     if verbose:
-        print("built", LIB_PATH)
+        print("built", LIB_PATH, "and", CEILING_LIB_PATH)
     return LIB_PATH
 
 

@@ -116,8 +116,9 @@ czip_status czip_prefill_cdf(czip_ctx* ctx, const uint32_t* targets, const int32
 
 /* ---- czip_prefill_cdf without allocation.  No counterpart in the
  *      reference: this is for callers that cannot allocate device memory
- *      (code under HIP graph capture, tight serving loops, harnesses that
- *      forbid hipMalloc).  The same (cum_lo, cum_hi) as czip_prefill_cdf, but
+ *      (tight serving loops, harnesses that forbid hipMalloc).  It runs
+ *      eagerly and synchronizes, so it cannot itself be captured into a HIP
+ *      graph.  The same (cum_lo, cum_hi) as czip_prefill_cdf, but
  *      targets [B*T], lens [B] and cum_lohi [B*T, 2] are DEVICE pointers on
  *      the context's device (4-, 4- and 8-byte aligned, as hipMalloc
  *      memory is), and every intermediate lives in one fixed
@@ -126,7 +127,10 @@ czip_status czip_prefill_cdf(czip_ctx* ctx, const uint32_t* targets, const int32
  *      B * T rows that need more than that give CZIP_E_RANGE (the shipped
  *      model needs ~3.5 KB per row: about 19K rows, e.g. 37 chunks of 512).
  *      lens are clamped to [0, T]; rows past a chunk's length come back 0; a
- *      target >= vocab in a live row gives CZIP_E_TOKEN.  Synchronous.  All
+ *      target >= vocab in a live row gives CZIP_E_TOKEN.  Synchronous: the
+ *      call first waits for all work queued on the device (its own stream
+ *      does not wait for the caller's), so inputs written asynchronously on
+ *      any stream before the call are complete when it reads them.  All
  *      calls on one GPU share its buffer, so calls that overlap in time on
  *      one GPU (several contexts or host threads) race. ---- */
 #define CZIP_NOALLOC_SCRATCH_BYTES (64ull << 20)

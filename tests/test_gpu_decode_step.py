@@ -146,5 +146,19 @@ def test_decode_step_errors(amd):
             gm.decode_step(np.array([1022, 5000, 1, 2], np.uint32), np.zeros(4, np.int32))
         assert e.value.code == -5
         assert not gm.decode_step(np.zeros(4, np.uint32), np.full(4, -1, np.int32)).any()
+        with pytest.raises(amd.CzipError) as e:
+            gm.decode_step(np.full(4, 1022, np.uint32), np.full(4, 1, np.int32))
+        assert e.value.code == -1  # position 0 never decoded
+        bos = np.full(4, 1022, np.uint32)
+        gm.decode_step(bos, np.array([0, 0, -1, -1], np.int32))
+        gm.decode_step(np.array([5, 6, 0, 0], np.uint32), np.array([1, 1, -1, -1], np.int32))
+        with pytest.raises(amd.CzipError) as e:
+            # stream 2 joins at position 2 with no cached keys before it
+            gm.decode_step(np.array([5, 6, 7, 0], np.uint32), np.array([2, 2, 2, -1], np.int32))
+        assert e.value.code == -1
+        # streams that begin at 0 (a new chunk) may join at any step, and a
+        # stream may repeat a position it has reached
+        gm.decode_step(bos, np.array([-1, -1, 0, 0], np.int32))
+        gm.decode_step(np.array([5, 6, 0, 0], np.uint32), np.array([1, 1, -1, -1], np.int32))
     finally:
         gm.decode_end()

@@ -7,7 +7,7 @@ import sys
 import numpy as np
 import pytest
 
-from conftest import MODEL_PATH
+from conftest import GQA_PIN_SHAPES, MODEL_PATH, gqa_pin_logits, write_gqa_pin_model
 
 pytestmark = pytest.mark.gpu
 
@@ -83,13 +83,17 @@ def test_cumfreqs_and_cdf_shipped(gpu_shipped, shipped):
 
 
 @pytest.mark.parametrize("chunk", [64, 512])
-def test_compress_bytes_shipped(gpu_shipped, shipped, chunk):
+def test_compress_bytes_shipped(amd, gpu_shipped, shipped, chunk):
     rng = np.random.default_rng(13 + chunk)
     n = chunk * 2 + chunk // 3
     toks = rng.integers(0, 1024, n).astype(np.uint32)
     _say(f"compress shipped chunk={chunk} n={n}")
     job = gpu_shipped.compress_plan(toks, chunk)
     try:
+        for fetch in (job.fetch, job.fetch_slots):  # nothing to fetch before the job has run
+            with pytest.raises(amd.CzipError) as e:
+                fetch()
+            assert e.value.code == -1
         job.run()
         got = job.fetch()  # packed on the device
         assert job.fetch_slots() == got  # the fixed-slot copy
@@ -189,9 +193,11 @@ def test_unfused_norm_path(amd, orc, tmp_path, monkeypatch):
     toks = synth.zipf_ids(sum(lens), 1024, seed=92)
     ref = orc.Model.from_file(MODEL_PATH).compress_many(toks, 64, threads=2)
     for tiled in (False, True):
-        # W-stationary requant / raw-logit GEMMs, then the tiled ones
+        # W-stationary requant / raw-logit GEMMs, then the tiled ones (the
+        # switch is read when a context is created)
         if tiled:
             monkeypatch.setenv("CZIP_GEMM_TILED", "1")
+            gm2 = amd.Model(amd.ModelWeights(MODEL_PATH))
         _say(f"compress shipped, unfused norms, tiled GEMMs {tiled}")
         assert gm2.compress_chunks(toks, 64) == ref
         out = gm2.decompress_chunks(ref, lens)
@@ -382,14 +388,16 @@ def test_decompress_attention_edge_cases(amd, orc, tmp_path):
     _roundtrip(amd, orc, path, amd.KV_RUST_COMPAT, toks, 200)
 
 
-def test_decompress_stream_groups(gpu_shipped, shipped, monkeypatch):
-    """More chunks than streams per group: groups run one after the other."""
+def test_decompress_stream_groups(amd, shipped, monkeypatch):
+    """More chunks than streams per group: groups run one after the other
+    (the cap is read when a context is created)."""
     monkeypatch.setenv("CZIP_DECODE_STREAMS", "3")
+    gm = amd.Model(amd.ModelWeights(MODEL_PATH))
     rng = np.random.default_rng(70)
     toks = rng.integers(0, 1024, 64 * 7 + 5).astype(np.uint32)
-    chunks = gpu_shipped.compress_chunks(toks, 64)
+    chunks = shipped.compress_many(toks, 64, threads=4)
     ntoks = [64] * 7 + [5]
-    out = gpu_shipped.decompress_chunks(chunks, ntoks)
+    out = gm.decompress_chunks(chunks, ntoks)
     assert np.array_equal(out, toks)
 
 
@@ -504,3 +512,35 @@ def test_vacc_wrap(amd, orc, tmp_path):
     ref = om.compress_many(toks, 512, threads=2)
     assert gm.compress_chunks(toks, 512) == ref
     assert np.array_equal(gm.decompress_chunks(ref, [512, 300]), toks)
+
+
+@pytest.mark.parametrize("H,G", GQA_PIN_SHAPES)
+def test_gqa_group_mapping_closed_form(amd, tmp_path, H, G):
+    """The device's GQA mode against the closed form of write_gqa_pin_model:
+    head h's attention output is floor(h G / H) + 1 (query head h on KV
+    group floor(h G / H), values from that group's V slice), seen through
+    the logits at every position of a full and a ragged chunk."""
+    path = write_gqa_pin_model(str(tmp_path / f"gqa{H}_{G}.czm"), H, G)
+    gm = amd.Model(amd.ModelWeights(path, amd.KV_GQA))
+    lens = [96, 33]
+    inp = np.zeros((2, 96), np.uint32)
+    inp[:, 0] = 1022
+    inp[:, 1:] = np.arange(1, 96) * 5
+    _say(f"gqa closed form H={H} G={G}")
+    got = gm.forward_logits(inp, lens)
+    exp = gqa_pin_logits(H, G)
+    for b, n in enumerate(lens):
+        assert (got[b, :n] == exp[None, :]).all(), f"chunk {b}"
+
+
+def test_gqa_one_group_equals_reference_slicing(amd, orc, tmp_path):
+    """With one KV group the device's GQA mode and its reference-slicing mode
+    give the oracle's reference-slicing chunk bytes."""
+    from czip_amd import synth
+    path = synth.write_random_model(str(tmp_path / "g1.czm"), d=384, n_layers=2, n_heads=6, n_kv=1, d_ff=512,
+                                    vocab=1024, ctx=128, seed=44)
+    toks = synth.zipf_ids(128 * 2 + 40, 1024, seed=45)
+    ref = orc.Model.from_file(path, orc.KV_RUST_COMPAT).compress_many(toks, 128, threads=4)
+    for kv in (amd.KV_GQA, amd.KV_RUST_COMPAT):
+        _say(f"one KV group, kv mode {kv}")
+        assert amd.Model(amd.ModelWeights(path, kv)).compress_chunks(toks, 128) == ref

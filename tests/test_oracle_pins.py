@@ -11,7 +11,7 @@ from fractions import Fraction
 import numpy as np
 import pytest
 
-from conftest import MODEL_PATH
+from conftest import GQA_PIN_SHAPES, MODEL_PATH, gqa_pin_logits, write_gqa_pin_model
 
 ACOEF = 378194  # ATTN_COEF_Q24 (attention.rs:17-19)
 CCOEF = 37819   # softmax.coef_q24 of the shipped model
@@ -293,3 +293,38 @@ def test_bpe_against_naive_merge(spec, orc):
         e = encode_piece(w.encode())
         assert ref.byte_pair_encode(w.encode()) == naive_bpe(w.encode(), ranks)
         assert prod.encode(w).tolist() == e, w
+
+
+@pytest.mark.parametrize("H,G", GQA_PIN_SHAPES)
+def test_gqa_group_mapping_closed_form(orc, tmp_path, H, G):
+    """GQA mode (the extension beyond attention.rs:172-194): with zero
+    queries and keys and KV group g's values all g + 1, head h's output is
+    floor(h G / H) + 1, which the logits of write_gqa_pin_model expose.  A
+    mapping h % G, or values taken from the key slice, gives other logits."""
+    path = write_gqa_pin_model(str(tmp_path / f"gqa{H}_{G}.czm"), H, G)
+    exp = gqa_pin_logits(H, G)
+    d = 64 * H
+    per_head = exp[:d].reshape(H, 64)
+    assert (per_head == per_head[:, :1]).all()
+    # distinct groups give distinct logits, so the check sees the grouping
+    groups = [h * G // H for h in range(H)]
+    vals = {g: int(per_head[h, 0]) for h, g in enumerate(groups)}
+    assert len(set(vals.values())) == G
+    if G not in (1, H):
+        assert [int(per_head[h, 0]) for h in range(H)] != [vals[h % G] for h in range(H)]
+    om = orc.Model.from_file(path, orc.KV_GQA)
+    inp = np.array([1022] + list(range(0, 700, 7))[:95], np.uint32)
+    lg, _ = om.trace(inp)
+    assert (lg == exp[None, :]).all()
+
+
+def test_gqa_one_group_equals_reference_slicing(orc, tmp_path):
+    """With one KV group, GQA mode and the reference's slicing
+    (attention.rs:174-194) read the same K and V: the same chunk bytes."""
+    from czip_amd import synth
+    path = synth.write_random_model(str(tmp_path / "g1.czm"), d=384, n_layers=2, n_heads=6, n_kv=1, d_ff=512,
+                                    vocab=1024, ctx=128, seed=44)
+    toks = synth.zipf_ids(128 * 2 + 40, 1024, seed=45)
+    a = orc.Model.from_file(path, orc.KV_GQA).compress_many(toks, 128, threads=4)
+    b = orc.Model.from_file(path, orc.KV_RUST_COMPAT).compress_many(toks, 128, threads=4)
+    assert a == b

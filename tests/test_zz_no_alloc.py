@@ -1,8 +1,9 @@
 """czip_prefill_cdf_noalloc (device buffers in, device buffers out, no
 allocation inside) against czip_prefill_cdf on the same inputs, bit for
-bit: two calls in a row, the second smaller, then the size and token
-errors.  Device memory for the inputs and outputs comes from the HIP
-runtime the library itself links (ctypes), not from the library."""
+bit, and on a few chunks against the oracle: two calls in a row, the
+second smaller, then the size and token errors.  Device memory for the
+inputs and outputs comes from the HIP runtime the library itself links
+(ctypes), not from the library."""
 import ctypes as C
 
 import numpy as np
@@ -68,7 +69,17 @@ def _noalloc(amd, gm, hip, tgt, lens):
         hip.free(d_t, d_l, d_o)
 
 
-def test_noalloc_equals_prefill_cdf(setup):
+def _oracle_lohi(om, tgt_row, n):
+    """The coder intervals of one chunk's first n targets from the oracle's
+    cumulative tables (inputs: BOS 1022, then the targets shifted by one)."""
+    inp = np.concatenate([[1022], tgt_row[:n - 1]]).astype(np.uint32)
+    _, cum = om.trace(inp)
+    t = tgt_row[:n].astype(np.int64)
+    lo = np.where(t > 0, cum[np.arange(n), np.maximum(t - 1, 0)], 0)
+    return np.stack([lo, cum[np.arange(n), t]], axis=1).astype(np.uint32)
+
+
+def test_noalloc_equals_prefill_cdf(setup, shipped):
     amd, gm, hip = setup
     rng = np.random.default_rng(120)
     for B, T, lens in [(12, 512, [512, 400, 1, 512, 511, 7, 512, 256, 300, 512, 64, 129]),
@@ -79,6 +90,11 @@ def test_noalloc_equals_prefill_cdf(setup):
         exp = gm.prefill_cdf(tgt, lens)
         assert np.array_equal(got, exp)
         assert (got[2, lens[2]:] == 0).all()
+        # and against the oracle, on a full chunk, a ragged one and a
+        # one-token one of the first call
+        for b in ([0, 1, 2] if B == 12 else [1]):
+            n = lens[b]
+            assert np.array_equal(got[b, :n], _oracle_lohi(shipped, tgt[b], n)), f"chunk {b}"
 
 
 def test_noalloc_limits(setup):
