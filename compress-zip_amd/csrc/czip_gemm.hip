@@ -590,22 +590,23 @@ void launch_gemm(const GemmArgs& a, int epi, hipStream_t s) {
 constexpr int RBM = 64;
 
 
-// Epilogue of the row GEMM for rows m0 .. m0 + 63 (all d columns in the
-// workgroup): requantize, residual add, both RMSNorms (model.rs:424-468).
+// Epilogue of the row GEMM for rows m0 .. m0 + 16 RT - 1 (all d columns in
+// the workgroup; RT = 4 row tiles in the 64-row kernels, 1 in the 16-row one):
+// requantize, residual add, both RMSNorms (model.rs:424-468).
 // Lane holds columns nb + 16 t + c4 .. +3 of rows m0 + 16 i + lr; w1r / w2r
 // are its columns' norm weights.  Its residual inputs (int16 stream or the
 // token's embedding row) are requested first so that their latency hides
 // behind step 1 and the first reduction; mid() runs after that reduction,
 // before the first store.
-template <int NW, int CT, bool FAST, class Mid>
-__device__ __forceinline__ void rn_epilogue(const RowGemmArgs& a, v4i (&acc)[4][CT], int m0, const unsigned (&w1r)[CT],
-                                            const unsigned (&w2r)[CT], unsigned (*red)[RBM], int* inv_s, Mid mid) {
+template <int NW, int CT, bool FAST, int RT, class Mid>
+__device__ __forceinline__ void rn_epilogue(const RowGemmArgs& a, v4i (&acc)[RT][CT], int m0, const unsigned (&w1r)[CT],
+                                            const unsigned (&w2r)[CT], unsigned (*red)[16 * RT], int* inv_s, Mid mid) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nb = wave * CT * 16;
     const int lr = lane & 15, c4 = (lane >> 4) * 4;
-    uint2 xr[4][CT];
+    uint2 xr[RT][CT];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < RT; i++) {
         const int row = min(m0 + i * 16 + lr, a.M - 1);
         if (a.x_in) {
 #pragma unroll
@@ -618,7 +619,7 @@ __device__ __forceinline__ void rn_epilogue(const RowGemmArgs& a, v4i (&acc)[4][
     }
     // 1. y = requant(acc); row sums of y^2
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < RT; i++) {
         unsigned ss = 0;
 #pragma unroll
         for (int t = 0; t < CT; t++)
@@ -634,7 +635,7 @@ __device__ __forceinline__ void rn_epilogue(const RowGemmArgs& a, v4i (&acc)[4][
     }
     __syncthreads();
     auto row_inv = [&]() {
-        if (wave == 0) {
+        if (wave == 0 && lane < 16 * RT) {
             unsigned s = 0;
 #pragma unroll
             for (int w = 0; w < NW; w++) s += red[w][lane];
@@ -647,7 +648,7 @@ __device__ __forceinline__ void rn_epilogue(const RowGemmArgs& a, v4i (&acc)[4][
     mid();
     // 2. x = x_in + rmsnorm(y, w1); keep clamp(x); row sums of clamp(x)^2
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < RT; i++) {
         const int row = m0 + i * 16 + lr;
         const bool live = row < a.M;
         const double inv = (double)inv_s[i * 16 + lr] * (1.0 / 32768.0);
@@ -683,7 +684,7 @@ __device__ __forceinline__ void rn_epilogue(const RowGemmArgs& a, v4i (&acc)[4][
     row_inv();
     // 3. xn = rmsnorm(clamp(x), w2)
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < RT; i++) {
         const int row = m0 + i * 16 + lr;
         if (row >= a.M) continue;
         const double inv = (double)inv_s[i * 16 + lr] * (1.0 / 32768.0);
@@ -809,6 +810,73 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_rn_ws(RowGemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Row GEMM for a few thousand rows (decode steps of a few thousand streams):
+// a workgroup owns 16 rows and all d columns, so M = 4096 rows fill the 256
+// CUs with no split of K (and no partial sums through HBM).  The rows' whole
+// A (16 x K bytes, K <= 4096) is staged in LDS at once; each wave streams its
+// CT column tiles of W (fragment-major) straight into registers WP K steps
+// ahead, every W operand used by one MFMA.  The epilogue is rn_epilogue over
+// one row tile.
+// ---------------------------------------------------------------------------
+constexpr int RN16_KMAX = 4096;
+constexpr int RN16_WP = 3;  // K steps of W in flight per wave
+
+template <int NW, int CT, bool FAST>
+__global__ __launch_bounds__(64 * NW) void k_gemm_rn16(RowGemmArgs a) {
+    __shared__ __attribute__((aligned(16))) int8_t As[RN16_KMAX / 64][1024];  // K step kt: [16 rows][64], lds64 rows
+    __shared__ unsigned red[NW][16];
+    __shared__ int inv_s[16];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15;
+    const int m0 = blockIdx.x * 16;
+    const int nb = wave * CT * 16;
+    const int c4 = (lane >> 4) * 4;
+    const int nkt = a.K / 64;
+    const int arows = min(a.M - m0, 16);
+    const __amdgpu_buffer_rsrc_t rA =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.A + (size_t)m0 * a.K), (short)0, arows * a.K, BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc((void*)a.Wf, (short)0, a.d * a.K, BUF_DWORD3);
+    const int woff = (nb >> 4) * nkt * 1024 + lane * 16;
+    v4i w[RN16_WP][CT];
+    auto fetch_w = [&](v4i* wr, int kt) {
+#pragma unroll
+        for (int t = 0; t < CT; t++) wr[t] = __builtin_amdgcn_raw_buffer_load_b128(rW, woff + t * nkt * 1024, kt * 1024, 0);
+    };
+#pragma unroll
+    for (int p = 0; p < RN16_WP - 1; p++)
+        if (p < nkt) fetch_w(w[p], p);
+    // chunk c: K step c / 64, row (c / 4) % 16, 16-byte piece c % 4 (rows past M read 0)
+    for (int c = tid; c < nkt * 64; c += 64 * NW) {
+        const int row = (c >> 2) & 15, pc = c & 3, kt = c >> 6;
+        const v4i x = __builtin_amdgcn_raw_buffer_load_b128(rA, row * a.K + kt * 64 + pc * 16, 0, 0);
+        *(v4i*)(As[kt] + lds64(row, pc)) = x;
+    }
+    unsigned w1r[CT], w2r[CT];
+#pragma unroll
+    for (int t = 0; t < CT; t++) {
+        w1r[t] = *(const unsigned*)(a.w1 + nb + t * 16 + c4);
+        w2r[t] = *(const unsigned*)(a.w2 + nb + t * 16 + c4);
+    }
+    __syncthreads();
+    v4i acc[1][CT];
+#pragma unroll
+    for (int t = 0; t < CT; t++) acc[0][t] = (v4i){0, 0, 0, 0};
+    // K step kt multiplies with w[kt % WP] after requesting step kt + WP - 1
+    for (int k0 = 0; k0 < nkt; k0 += RN16_WP) {
+#pragma unroll
+        for (int u = 0; u < RN16_WP; u++) {
+            const int kt = k0 + u;
+            if (kt < nkt) {
+                if (kt + RN16_WP - 1 < nkt) fetch_w(w[(u + RN16_WP - 1) % RN16_WP], kt + RN16_WP - 1);
+                const v4i af = *(const v4i*)(As[kt] + lds64(lr, lane >> 4));
+#pragma unroll
+                for (int t = 0; t < CT; t++) acc[0][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[u][t], af, acc[0][t], 0, 0, 0);
+            }
+        }
+    }
+    rn_epilogue<NW, CT, FAST>(a, acc, m0, w1r, w2r, red, inv_s, [] {});
+}
+
+// ---------------------------------------------------------------------------
 // Split-K row GEMM for few rows (decode with a few thousand streams): the
 // workgroup (row block, K slice) multiplies its K steps and stores the int32
 // partial sums; k_rn_splitk_epi then sums the slices and runs the row GEMM's
@@ -882,8 +950,26 @@ static void launch_rn_ws(const RowGemmArgs& a, hipStream_t s) {
         hipLaunchKernelGGL((k_gemm_rn_ws<NW, CT, KS, false>), grid, dim3(64 * NW), 0, s, a);
 }
 
+// few 64-row blocks but at least RN16_MIN_BLOCKS blocks of 16 rows: one
+// workgroup per 16 rows, K unsplit
+constexpr int RN16_MIN_BLOCKS = 96;
+static bool use_rn16(const RowGemmArgs& a) {
+    const int nblk = (a.M + RBM - 1) / RBM;
+    return nblk < 96 && (a.M + 15) / 16 >= RN16_MIN_BLOCKS && a.K <= RN16_KMAX;
+}
+
 template <int NW, int CT>
 static void launch_rn(const RowGemmArgs& a, hipStream_t s) {
+    if (use_rn16(a)) {
+        // 8 waves of d / 128 tiles where that divides (else the 64-row kernel's split)
+        constexpr int TILES = NW * CT;
+        constexpr int NW16 = TILES % 8 == 0 && TILES / 8 <= 8 ? 8 : NW, CT16 = TILES / NW16;
+        static_assert(NW16 * CT16 == NW * CT, "the 16-row kernel splits the same d columns");
+        const dim3 grid((unsigned)((a.M + 15) / 16));
+        if (a.rq_fast) hipLaunchKernelGGL((k_gemm_rn16<NW16, CT16, true>), grid, dim3(64 * NW16), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_rn16<NW16, CT16, false>), grid, dim3(64 * NW16), 0, s, a);
+        return;
+    }
     if (try_rn_splitk<NW, CT>(a, s)) return;
     dim3 grid((unsigned)((a.M + RBM - 1) / RBM));
     const bool full = a.K <= 1024;
@@ -899,7 +985,7 @@ static void launch_rn(const RowGemmArgs& a, hipStream_t s) {
 // d = 64 h columns over NW waves of CT 16-wide tiles: 8 waves where h is even
 // (few accumulators per wave, many waves to hide the W stream's latency)
 void launch_gemm_rn(const RowGemmArgs& a, hipStream_t s) {
-    if (!a.tiled && a.d == 384 && a.M > 0 && (long long)a.M * a.K < (1ll << 40)) {
+    if (!a.tiled && a.d == 384 && a.M > 0 && (long long)a.M * a.K < (1ll << 40) && !use_rn16(a)) {
         if (a.K == 384) { launch_rn_ws<8, 3, 6>(a, s); return; }
         if (a.K == 512) { launch_rn_ws<8, 3, 8>(a, s); return; }
     }

@@ -544,3 +544,26 @@ def test_gqa_one_group_equals_reference_slicing(amd, orc, tmp_path):
     for kv in (amd.KV_GQA, amd.KV_RUST_COMPAT):
         _say(f"one KV group, kv mode {kv}")
         assert amd.Model(amd.ModelWeights(path, kv)).compress_chunks(toks, 128) == ref
+
+
+@pytest.mark.parametrize("n_chunks,chunk", [(4, 512), (33, 64), (95, 64), (1600, 64)])
+def test_small_launch_row_gemm(gpu_shipped, shipped, n_chunks, chunk):
+    """Launches of a few thousand rows (fewer than 96 blocks of 64 rows, at
+    least 96 of 16) take the 16-row row GEMM for the O and down projections:
+    prefill launches of 2,048, 2,112 and 6,075 rows (logits against the
+    oracle, then the compressed bytes), and decode steps of 1,600 streams (the
+    chunks decoded back)."""
+    rng = np.random.default_rng(300 + n_chunks)
+    lens = [chunk] * (n_chunks - 1) + [chunk - 5]
+    toks = rng.integers(0, 1024, sum(lens)).astype(np.uint32)
+    if n_chunks < 100:
+        inp, _ = _chunk_inputs(toks, lens, chunk)
+        _say(f"row GEMM 16-row blocks, prefill: {n_chunks} x {chunk}")
+        got = gpu_shipped.forward_logits(inp, lens)
+        for b in (0, n_chunks // 2, n_chunks - 1):
+            ref, _ = shipped.trace(inp[b, :lens[b]])
+            assert np.array_equal(got[b, :lens[b]], ref), f"chunk {b}"
+    ref = shipped.compress_many(toks, chunk, threads=8)
+    _say(f"row GEMM 16-row blocks, compress + decode: {n_chunks} x {chunk}")
+    assert gpu_shipped.compress_chunks(toks, chunk) == ref
+    assert np.array_equal(gpu_shipped.decompress_chunks(ref, lens), toks)
