@@ -155,15 +155,22 @@ def ceilings():
     L = C.CDLL(b.CEILING_LIB_PATH)
     L.czc_copy_gbs.argtypes = [C.c_size_t, C.c_int, C.POINTER(C.c_double)]
     L.czc_mfma_i8_tops.argtypes = [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double)]
-    gbs, t32, t16 = C.c_double(), C.c_double(), C.c_double()
-    if (L.czc_copy_gbs(1 << 30, 10, C.byref(gbs)) or L.czc_mfma_i8_tops(32, 6000, 8, C.byref(t32))
-            or L.czc_mfma_i8_tops(16, 3000, 8, C.byref(t16))):
-        raise SystemExit("ceiling probes failed")
-    return {"hbm_copy_gbs": round(gbs.value, 1), "int8_mfma_tops": round(t32.value, 1),
-            "int8_mfma_16x16x64_tops": round(t16.value, 1),
-            "copy": "1 GiB device-to-device copy kernel, 16-byte loads/stores, 4 workgroups per CU, 10 timed passes",
+    best = {"copy": 0.0, 32: 0.0, 16: 0.0}
+    v = C.c_double()
+    for _ in range(3):  # the best of three: the clock under a long MFMA loop varies between runs and boxes
+        if L.czc_copy_gbs(1 << 30, 10, C.byref(v)):
+            raise SystemExit("copy ceiling probe failed")
+        best["copy"] = max(best["copy"], v.value)
+        for shape, iters in ((32, 4000), (16, 2000)):
+            if L.czc_mfma_i8_tops(shape, iters, 8, C.byref(v)):
+                raise SystemExit("MFMA ceiling probe failed")
+            best[shape] = max(best[shape], v.value)
+    return {"hbm_copy_gbs": round(best["copy"], 1), "int8_mfma_tops": round(best[32], 1),
+            "int8_mfma_16x16x64_tops": round(best[16], 1),
+            "copy": "1 GiB device-to-device copy kernel, 16-byte loads/stores, 4 workgroups per CU, 10 timed passes, "
+                    "best of 3",
             "mfma": "v_mfma_i32_32x32x32_i8, 4 independent chains per wave (16x16x64: 16 chains), "
-                    "8 waves per SIMD, no memory traffic"}
+                    "8 waves per SIMD, no memory traffic, best of 3"}
 
 
 def main():
