@@ -23,6 +23,19 @@ __global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, u
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
 }
 
+// the sum of n 16-byte words, a grid-stride loop of 16-byte loads (read-only
+// traffic: HBM reads without the write turnarounds of a copy); one word per
+// workgroup is stored so that nothing is dead
+__global__ __launch_bounds__(256) void k_read16(const uint4* __restrict__ src, size_t n, unsigned* __restrict__ out) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    unsigned acc = 0;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const uint4 v = src[i];
+        acc += v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;  // practically never taken, but not provably dead
+}
+
 // NC independent accumulator chains per wave, `iters` rounds of NC MFMAs on
 // register operands; the sums are stored so that nothing is dead
 template <int NC>
@@ -108,6 +121,41 @@ done:
     if (e1) hipEventDestroy(e1);
     if (src) hipFree(src);
     if (dst) hipFree(dst);
+    return rc;
+}
+
+// Read `bytes` (a multiple of 16) `reps` times after one untimed pass; *gbs =
+// bytes read / time of the timed passes.  0 on success.
+int czc_read_gbs(size_t bytes, int reps, double* gbs) {
+    if (bytes < 16 || bytes % 16 != 0 || reps < 1 || !gbs) return -2;
+    void* src = nullptr;
+    unsigned* out = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = -1;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        return -1;
+    if (hipMalloc(&src, bytes) != hipSuccess || hipMalloc(&out, (size_t)cus * 8 * sizeof(unsigned)) != hipSuccess) goto done;
+    if (hipMemset(src, 1, bytes) != hipSuccess || hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+        goto done;
+    {
+        const size_t n = bytes / 16;
+        const dim3 grid(8 * cus), block(256);
+        hipLaunchKernelGGL(k_read16, grid, block, 0, 0, (const uint4*)src, n, out);
+        hipEventRecord(e0, 0);
+        for (int r = 0; r < reps; r++) hipLaunchKernelGGL(k_read16, grid, block, 0, 0, (const uint4*)src, n, out);
+        hipEventRecord(e1, 0);
+        float ms = 0;
+        if (hipGetLastError() != hipSuccess || timed_ms(e0, e1, &ms)) goto done;
+        *gbs = (double)bytes * reps / (ms * 1e-3) / 1e9;
+        rc = 0;
+    }
+done:
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (src) hipFree(src);
+    if (out) hipFree(out);
     return rc;
 }
 

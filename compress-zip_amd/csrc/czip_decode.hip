@@ -218,10 +218,12 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int G
     };
     if constexpr (NS == 1) {
         // two register sets: the tile's operands in one while the next tile's
-        // are loaded into the other; the last tile reloads itself, so the loads
-        // stay unconditional and nothing waits on them before their use
+        // are loaded into the other; after the last tile the loads stay
+        // unconditional (nothing waits on them before their use) but point
+        // past the stream's cache, where the range check returns zeros
+        // without reading memory
         auto tile = [&](v4i* kc, v4i* vc, v4i* kn, v4i* vn, int t0) {
-            const int tn = t0 + 64 <= p ? t0 + 64 : t0;
+            const int tn = t0 + 64 <= p ? t0 + 64 : a.TP;
             attn_tile<GEN, 1, 64>(
                 [&](int, int blk) {
                     kn[blk] = load_k(0, blk, tn);
@@ -269,8 +271,11 @@ __global__ __launch_bounds__(256, 3) void k_attn_decode(AttnArgs a, int p, int G
             // the next tile's K and V once the passes are done: no operand
             // register is live across the passes (168 VGPRs, three waves per
             // SIMD; the next K requested after the scan held 210, two waves).
-            // The last full tile reloads itself (unconditional loads).
-            load_full(kt + 1 < nfull ? t0 + 64 : t0);
+            // After the last full tile the loads stay unconditional but point
+            // past the stream's cache (TP keys), where the range check returns
+            // zeros without reading memory (a reload of the tile itself went
+            // to HBM again: ~8 KB more per stream-step).
+            load_full(kt + 1 < nfull ? t0 + 64 : a.TP);
         }
         if (half_last) {
             // requested here, not in the loop: their offsets would stay live
