@@ -87,6 +87,8 @@ def main(n_chunks: int = 64, T: int = 512):
 
     hist = collections.defaultdict(collections.Counter)
     cols = collections.defaultdict(list)
+    octets = np.zeros(8)  # splits in the first key tile by key octet, rows 64.. (which see all 64 keys)
+    n_rows = 0
     causal = np.tril(np.ones((T, T), bool))
     for c in range(n_chunks):
         toks = ids[c * T:(c + 1) * T]
@@ -101,6 +103,8 @@ def main(n_chunks: int = 64, T: int = 512):
             prev = np.maximum.accumulate(sc, axis=1)
             split = np.zeros_like(sc, bool)
             split[:, 1:] = sc[:, 1:] > prev[:, :-1]
+            octets += split[64:, :64].reshape(T - 64, 8, 8).sum(axis=(0, 2))
+            n_rows += T - 64
             for b in range(T // 16):
                 r0, last = 16 * b, (16 * b + 15) // 64
                 for kt in range(last + 1):
@@ -119,7 +123,8 @@ def main(n_chunks: int = 64, T: int = 512):
         tot_passes += p
         res[name] = {"tiles": n, "mean_passes": round(p / n, 2), "mean_useful_columns": round(float(np.mean(cols[name])), 1),
                      "passes_histogram": {int(k): h[k] for k in sorted(h)}}
-    res["all"] = {"tiles": tot_tiles, "mean_passes": round(tot_passes / tot_tiles, 2), "chunks": n_chunks, "heads": H}
+    res["all"] = {"tiles": tot_tiles, "mean_passes": round(tot_passes / tot_tiles, 2), "chunks": n_chunks, "heads": H,
+                  "first_tile_splits_per_row_by_key_octet": [round(float(x) / n_rows, 2) for x in octets]}
     print(json.dumps(res, indent=1))
 
 
