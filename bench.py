@@ -24,13 +24,14 @@ import numpy as np  # noqa: E402
 PEAK_INT8_TOPS = 5000.0     # TOP/s
 PEAK_HBM_GBS = 8000.0       # GB/s
 
-# The commit the two profile-derived constants below were measured at (they go
-# stale when the kernels change; the bench line carries this name with them).
-PROFILED_AT = "f52d556"
+# The commits the two profile-derived constants below were measured at (they go
+# stale when the kernels change; the bench line carries these names with them).
+TRAFFIC_PROFILED_AT = "8ff5e02"
+VALU_PROFILED_AT = "f52d556"
 # HBM bytes per token (read + write) of each kernel on the text workload, from
 # two rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0: the factors a
 # plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text.md
-TRAFFIC_B_PER_TOKEN = {"attention": 515 + 402, "qkv_table": 12 + 512, "gemm_o_norm": 396 + 1152,
+TRAFFIC_B_PER_TOKEN = {"attention": 516 + 411, "qkv_table": 12 + 512, "gemm_o_norm": 396 + 1152,
                        "ffn": 1440 + 384, "gemm_down_norm": 1946 + 384, "gemm_up": 677 + 1024, "head_cdf": 389 + 8}
 TRAFFIC_WORKLOADS = ("v001_L4_ctx512_text64MiB",)
 # Prefill attention: wave64 VALU instructions (MFMA excluded) per 16-row tile (64 keys, or
@@ -295,10 +296,10 @@ def main():
     if args.workload in TRAFFIC_WORKLOADS and roof["kernel"] in TRAFFIC_B_PER_TOKEN:
         per_launch_tokens = n / (kernels[dom]["launches"] / prof_steps)
         roof["traffic"] = round(TRAFFIC_B_PER_TOKEN[roof["kernel"]] * per_launch_tokens)
-        roof["traffic_source"] = (f"rocprofv3 FETCH_SIZE/WRITE_SIZE per token (profiled at {PROFILED_AT}) "
+        roof["traffic_source"] = (f"rocprofv3 FETCH_SIZE/WRITE_SIZE per token (profiled at {TRAFFIC_PROFILED_AT}) "
                                   f"x tokens per launch")
     if "valu" in roof:
-        roof["valu"]["profiled_at"] = PROFILED_AT
+        roof["valu"]["profiled_at"] = VALU_PROFILED_AT
     # the same rate against the measured ceiling of its resource
     roof["frac_of_measured"] = round(roof["achieved"] / (ceil["int8_mfma_tops"] if roof["bound"] == "mfma"
                                                          else ceil["hbm_copy_gbs"]), 5)
