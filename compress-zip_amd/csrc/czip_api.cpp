@@ -23,9 +23,12 @@ namespace {
 constexpr uint32_t BOS = 1022u;  // main.rs:222, 387
 constexpr int FFN_MIN_ROWS = 1 << 19;  // rows from which a layer's FFN runs as one fused kernel
 // device memory a job may use beyond its inputs and outputs (CZIP_SCRATCH_GB):
-// a compress sub-batch, or a decode group's caches; 32 GB of the 288 GB
-// halves the shipped model's 64 MiB-text job to 7 sub-batches (+0.5% against 16)
-constexpr double SCRATCH_GB_DEFAULT = 32.0;
+// a compress sub-batch, or a decode group's caches.  64 GB of the 288 GB holds
+// the caches of 2,048 streams of 4,096 tokens of the d768/L12 GQA model (51.5
+// GB) as one decode group (0.377 M tok/s, against 0.289 as the two groups of
+// a 32 GB budget: each step's launches are twice as wide), and compresses the
+// shipped model's 64 MiB text in 4 sub-batches (0.3% faster than 7 at 32 GB)
+constexpr double SCRATCH_GB_DEFAULT = 64.0;
 constexpr int DEC_LANES_MAX = 4;  // most HIP streams a decode group is split over
 // V^T block exponent of the decode caches (vt_off): a step appends one key, whose 64 value
 // bytes span 256 bytes with 4-key blocks (1 KB with the prefill caches' 16-key blocks); the

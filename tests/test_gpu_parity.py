@@ -546,13 +546,14 @@ def test_gqa_one_group_equals_reference_slicing(amd, orc, tmp_path):
         assert amd.Model(amd.ModelWeights(path, kv)).compress_chunks(toks, 128) == ref
 
 
-@pytest.mark.parametrize("n_chunks,chunk", [(4, 512), (33, 64), (95, 64), (1600, 64)])
+@pytest.mark.parametrize("n_chunks,chunk", [(4, 512), (33, 64), (95, 64), (1600, 64), (369, 64), (368, 64)])
 def test_small_launch_row_gemm(gpu_shipped, shipped, n_chunks, chunk):
     """Launches of a few thousand rows (fewer than 96 blocks of 64 rows, at
-    least 96 of 16) take the 16-row row GEMM for the O and down projections:
+    least 24 of 16) take the 16-row row GEMM for the O and down projections:
     prefill launches of 2,048, 2,112 and 6,075 rows (logits against the
-    oracle, then the compressed bytes), and decode steps of 1,600 streams (the
-    chunks decoded back)."""
+    oracle, then the compressed bytes), and decode steps of 1,600 and 369
+    streams (the chunks decoded back); 368 streams (23 blocks) stay on the
+    split-K kernels."""
     rng = np.random.default_rng(300 + n_chunks)
     lens = [chunk] * (n_chunks - 1) + [chunk - 5]
     toks = rng.integers(0, 1024, sum(lens)).astype(np.uint32)
