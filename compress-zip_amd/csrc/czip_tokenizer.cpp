@@ -10,13 +10,14 @@
 //
 // is executed by a hand-written scanner that tries the alternatives in order
 // at each position with the same possessive / backtracking semantics, so no
-// regex engine is needed.  The merge loop follows _byte_pair_merge
-// (tiktoken.rs:26-82).
+// regex engine is needed.  The merges give the ids _byte_pair_merge
+// (tiktoken.rs:26-82) gives, by a heap of candidate pairs.
 #include <dlfcn.h>
 
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <queue>
 #include <string>
 #include <thread>
 #include <unordered_map>
@@ -191,39 +192,49 @@ Rank rank_of(const czip_tokenizer* t, const uint8_t* p, size_t len) {
     return it == t->enc.end() ? RANK_MAX : it->second;
 }
 
-// tiktoken.rs:26-107
+// Byte-pair encoding of one pre-split piece, to the result tiktoken.rs:26-107
+// defines: from single bytes, merge the adjacent pair of parts whose
+// concatenation has the lowest rank (the leftmost such pair on a tie) until no
+// adjacent concatenation is a token; the ids are the parts' ranks.  Parts are
+// a linked list over their start offsets; every pair formed goes into a
+// min-heap ordered by (rank, start), and a popped pair whose span no longer
+// matches the current parts (one of them has since merged) is dropped, so a
+// piece of n bytes costs O(n log n) rank lookups.
 bool byte_pair_encode(const czip_tokenizer* t, const uint8_t* piece, size_t len, std::vector<Rank>& out) {
-    if (len == 1) {
-        Rank r = rank_of(t, piece, 1);
-        if (r == RANK_MAX) return false;
-        out.push_back(r);
-        return true;
+    if (len == 0) return true;
+    if (len > UINT32_MAX - 1) return false;
+    const uint32_t n = (uint32_t)len, none = UINT32_MAX;
+    std::vector<uint32_t> nxt(n), prv(n);  // start of the next / previous part (n after the last, none before the first)
+    std::vector<uint8_t> alive(n, 1);
+    for (uint32_t s = 0; s < n; s++) {
+        nxt[s] = s + 1;
+        prv[s] = s ? s - 1 : none;
     }
-    std::vector<std::pair<size_t, Rank>> parts;
-    parts.reserve(len + 1);
-    std::pair<Rank, size_t> mn{RANK_MAX, (size_t)-1};
-    for (size_t i = 0; i + 1 < len; i++) {
-        Rank r = rank_of(t, piece + i, 2);
-        if (r < mn.first) mn = {r, i};
-        parts.push_back({i, r});
-    }
-    parts.push_back({len - 1, RANK_MAX});
-    parts.push_back({len, RANK_MAX});
-    auto get_rank = [&](size_t i) -> Rank {
-        if (i + 3 < parts.size()) return rank_of(t, piece + parts[i].first, parts[i + 3].first - parts[i].first);
-        return RANK_MAX;
+    struct Pair {
+        Rank r;
+        uint32_t s, e;  // bytes [s, e): the part at s and the one after it
     };
-    while (mn.first != RANK_MAX) {
-        const size_t i = mn.second;
-        if (i > 0) parts[i - 1].second = get_rank(i - 1);
-        parts[i].second = get_rank(i);
-        parts.erase(parts.begin() + (long)(i + 1));
-        mn = {RANK_MAX, (size_t)-1};
-        for (size_t k = 0; k + 1 < parts.size(); k++)
-            if (parts[k].second < mn.first) mn = {parts[k].second, k};
+    auto later = [](const Pair& a, const Pair& b) { return a.r != b.r ? a.r > b.r : a.s > b.s; };
+    std::priority_queue<Pair, std::vector<Pair>, decltype(later)> heap(later);
+    auto offer = [&](uint32_t s) {  // the pair starting at part s, if it is a token
+        const uint32_t m = nxt[s];
+        if (m >= n) return;
+        const Rank r = rank_of(t, piece + s, nxt[m] - s);
+        if (r != RANK_MAX) heap.push({r, s, nxt[m]});
+    };
+    for (uint32_t s = 0; s + 1 < n; s++) offer(s);
+    while (!heap.empty()) {
+        const Pair p = heap.top();
+        heap.pop();
+        if (!alive[p.s] || nxt[p.s] >= n || nxt[nxt[p.s]] != p.e) continue;  // stale
+        alive[nxt[p.s]] = 0;
+        nxt[p.s] = p.e;
+        if (p.e < n) prv[p.e] = p.s;
+        if (prv[p.s] != none) offer(prv[p.s]);
+        offer(p.s);
     }
-    for (size_t k = 0; k + 1 < parts.size(); k++) {
-        Rank r = rank_of(t, piece + parts[k].first, parts[k + 1].first - parts[k].first);
+    for (uint32_t s = 0; s < n; s = nxt[s]) {
+        const Rank r = rank_of(t, piece + s, nxt[s] - s);
         if (r == RANK_MAX) return false;
         out.push_back(r);
     }

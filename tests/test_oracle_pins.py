@@ -266,7 +266,8 @@ def test_bpe_against_naive_merge(spec, orc):
     """The product's BPE and the oracle's restated merge loop both equal the
     naive lowest-rank merge (after the whole-piece lookup of tiktoken.rs:249-256)
     on every pre-split piece of a text and on random letter strings (each a
-    single piece), with the shipped model's 1022 ranks."""
+    single piece, 2-39 letters and 100-399 letters), with the shipped model's
+    1022 ranks."""
     import czip_amd
     import tokenizer_oracle as TO
     from czip_amd import synth
@@ -287,8 +288,9 @@ def test_bpe_against_naive_merge(spec, orc):
         exp.extend(e)
     assert prod.encode(text).tolist() == exp
     rng = np.random.default_rng(6)
-    for _ in range(1500):
-        w = "".join(chr(97 + c) for c in rng.integers(0, 26, int(rng.integers(2, 40))))
+    for i in range(1560):
+        n = int(rng.integers(2, 40)) if i < 1500 else int(rng.integers(100, 400))
+        w = "".join(chr(97 + c) for c in rng.integers(0, 26, n))
         assert ref.pieces(w) == [w]
         e = encode_piece(w.encode())
         assert ref.byte_pair_encode(w.encode()) == naive_bpe(w.encode(), ranks)
