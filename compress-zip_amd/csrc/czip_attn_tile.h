@@ -479,20 +479,23 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
         // rows (bit r, from lane r) that rescale at record j (none in pass 0)
         const unsigned long long resc = __builtin_amdgcn_ballot_w64(erow != 0u);
         wave_lds_fence();
-        // 4b. vacc (lanes = head dims).  Every row adds: a row without a
-        // segment j has w = 0 (bytes -128) in every column, so its product is
-        // exactly -corr and it adds 0.
+        // 4b. vacc (lanes = head dims).  Pass 0: every row adds its segment
+        // 0.  Pass j >= 1: only the rows with a segment j, which are the rows
+        // that rescale at record j (factors are at least 1); a row without
+        // one has w = 0 (bytes -128) in every column, its product is exactly
+        // -corr and it would add 0.
         unsigned bv[NR];
 #pragma unroll
         for (int r = 0; r < NR; r++) bv[r] = W.buf[r][lane];
-        if (resc) {
+        if (j == 0) {
+#pragma unroll
+            for (int r = 0; r < NR; r++) st.vacc[r] += bv[r] + corr;
+        } else {
 #pragma unroll
             for (int r = 0; r < NR; r++)
                 if ((resc >> r) & 1ull)
-                    st.vacc[r] = rescale_v(st.vacc[r], (unsigned)__builtin_amdgcn_readlane((int)erow, r));
+                    st.vacc[r] = rescale_v(st.vacc[r], (unsigned)__builtin_amdgcn_readlane((int)erow, r)) + bv[r] + corr;
         }
-#pragma unroll
-        for (int r = 0; r < NR; r++) st.vacc[r] += bv[r] + corr;
         wave_lds_fence();
     }
 }
