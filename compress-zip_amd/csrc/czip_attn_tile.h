@@ -434,11 +434,9 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
         unsigned erow = 0u;
         if (j >= 1) {
             if constexpr (NS == 1) {
-                // lowest split left: the low word's, else the high word's,
-                // else slot 64, which holds factor 0 (attn_wave_init) for a
-                // row with no split left
-                const unsigned lo = (unsigned)rsp, hi = (unsigned)(rsp >> 32);
-                const unsigned key = lo ? (unsigned)__builtin_ctzg(lo, 32) : 32u + (unsigned)__builtin_ctzg(hi, 32);
+                // lowest split left, else slot 64, which holds factor 0
+                // (attn_wave_init) for a row with no split left
+                const unsigned key = (unsigned)__builtin_ctzg(rsp, 64);
                 erow = (unsigned)W.ex[row][key] ^ WB;
                 rsp &= rsp - 1ull;
             } else {
