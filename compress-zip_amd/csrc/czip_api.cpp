@@ -99,6 +99,7 @@ struct czip_ctx {
     double scratch_gb = 0;        // CZIP_SCRATCH_GB: a job's scratch budget
     int64_t decode_streams = 0;   // CZIP_DECODE_STREAMS: most streams per decode group (0: no cap)
     int decode_lanes = 0;         // CZIP_DECODE_LANES: lanes per decode group (0: by group size)
+    bool lut0_max = false;        // exp2_lut[0] == 65535: the heads' table step 0 is E(0) (HeadCdfArgs::e0)
     std::vector<void*> allocs;
     int8_t *embed = nullptr, *final_norm = nullptr, *head_w = nullptr, *head_wf = nullptr;
     int8_t* embed_xn = nullptr;  // rmsnorm(embed[v], layer 0's attn_norm) for every token v
@@ -396,6 +397,7 @@ extern "C" czip_status czip_create(const czip_model_desc* w, int device, czip_ct
     UP(c->head_w, w->head_w, V * d)
     if ((rc = upload_frag_major(C, &c->head_wf, w->head_w, V, d))) return rc;
     UP(c->lut, w->exp2_lut, 256)
+    c->lut0_max = w->exp2_lut[0] == 65535;
     {
         std::vector<uint16_t> et(ETB_PAD);
         attn_etab_host(w->exp2_lut, et.data());
@@ -867,7 +869,7 @@ static czip_status run_compress(czip_job* j) {
         if (c->head_fused) {
             HeadCdfArgs h{};
             h.A = j->xn; h.W = c->head_wf; h.M = M; h.K = c->cfg.d_model; h.V = V; h.targets = j->tgt; h.lens = j->lens;
-            h.T = T; h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total;
+            h.T = T; h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total; h.e0 = c->lut0_max;
             h.out = j->lohi_all; h.out_row0 = c0 * T;
             Timed t(c, "head_cdf");
             launch_head_cdf(h, s);
@@ -1147,7 +1149,7 @@ static czip_status run_decompress(czip_job* j) {
                 if (c->head_fused) {
                     HeadDecArgs h{};
                     h.A = Ln.r.xn; h.W = c->head_wf; h.M = M; h.K = d; h.V = V;
-                    h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total; h.p = p;
+                    h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total; h.e0 = c->lut0_max; h.p = p;
                     Timed t(c, "head_dec");
                     launch_head_dec(h, Ln.st, Ln.ds, s);
                 } else {
@@ -1418,7 +1420,7 @@ extern "C" czip_status czip_prefill_cdf_noalloc(czip_ctx* c, const uint32_t* d_t
     if (c->head_fused) {
         HeadCdfArgs h{};
         h.A = j.xn; h.W = c->head_wf; h.M = M; h.K = c->cfg.d_model; h.V = V; h.targets = j.tgt; h.lens = j.lens;
-        h.T = T; h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total;
+        h.T = T; h.lut = c->lut; h.coef = c->cfg.coef_q24; h.total = c->cfg.target_total; h.e0 = c->lut0_max;
         h.out = d_cum_lohi; h.out_row0 = 0;
         Timed t(c, "head_cdf");
         launch_head_cdf(h, s);

@@ -523,7 +523,7 @@ void launch_cdf_decode(const int32_t* logits, int S, int V, const uint16_t* lut,
 //   - wave 0 stores the symbol and the interval; the next step's input
 //     kernel narrows and renormalizes the decoder (arith_coder.rs:243-262).
 // ---------------------------------------------------------------------------
-template <int CT>
+template <int CT, bool E0>
 __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState st, DecStreams ds) {
     __shared__ HeadLdsT<1> L;
     __shared__ unsigned row_v[HBM_ROWS], row_rem[HBM_ROWS], row_lo[HBM_ROWS], row_hi[HBM_ROWS];
@@ -547,7 +547,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
     __builtin_amdgcn_s_waitcnt(0);  // the block's A (and everything before) has landed
     __syncthreads();
     v4i acc[4][CT];
-    head_freqs<CT>(tid, L.As[0], a.K, a.W, a.V, a.coef, a.total, L, acc);
+    head_freqs<CT, E0>(tid, L.As[0], a.K, a.W, a.V, a.coef, a.total, L, acc);
     // sum f per row and wave
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -641,7 +641,8 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
 // up finish sooner than a fixed share per workgroup)
 void launch_head_dec(const HeadDecArgs& a, DecState st, DecStreams ds, hipStream_t s) {
     dim3 grid((unsigned)((a.M + HBM_ROWS - 1) / HBM_ROWS));
-    hipLaunchKernelGGL(k_head_dec<4>, grid, dim3(64 * HNW), 0, s, a, st, ds);
+    if (a.e0) hipLaunchKernelGGL((k_head_dec<4, true>), grid, dim3(64 * HNW), 0, s, a, st, ds);
+    else hipLaunchKernelGGL((k_head_dec<4, false>), grid, dim3(64 * HNW), 0, s, a, st, ds);
 }
 
 }  // namespace czip

@@ -88,8 +88,10 @@ __device__ __forceinline__ void head_stage_a(const int8_t* A, int M, int K, int 
 // (total - sum f) is left to the caller.
 // tid: threadIdx.x, passed in so that a persistent caller can make it opaque
 // per block (the lane-dependent addresses are then formed per block instead
-// of being held in registers across the whole loop).
-template <int CT, class Lds>
+// of being held in registers across the whole loop).  E0: lut[0] == 65535,
+// so step 0 (where a logit equal to the max lands) already reads 65535 and
+// the max needs no entry of its own.
+template <int CT, bool E0, class Lds>
 __device__ __forceinline__ void head_freqs(int tid, const int8_t (*As)[HBM_ROWS * 64], int K, const int8_t* W, int V,
                                            unsigned coef, unsigned total, Lds& L, v4i (&acc)[4][CT]) {
     const int wave = tid >> 6, lane = tid & 63;
@@ -145,7 +147,7 @@ __device__ __forceinline__ void head_freqs(int tid, const int8_t (*As)[HBM_ROWS 
                 const int l = acc[i][t][r];
                 ak = l == mx ? t * 4 + r : ak;
                 const unsigned st = min((unsigned)((unsigned long long)((long long)l * (long long)negc + kr) >> 32), 4096u);
-                const unsigned e = L.etab[l == mx ? ETAB_N - 1 : (int)st];
+                const unsigned e = L.etab[E0 || l != mx ? (int)st : ETAB_N - 1];
                 acc[i][t][r] = (int)e;
                 s += e;
             }

@@ -13,7 +13,7 @@ namespace czip {
 // Persistent: a workgroup (one per CU) walks row blocks blockIdx.x,
 // + gridDim.x, ..., the next block's A arriving in LDS by DMA while the
 // current one is reduced.
-template <int CT>
+template <int CT, bool E0>
 __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
     __shared__ HeadLdsT<2> L;
     const int nblk = (a.M + HBM_ROWS - 1) / HBM_ROWS;
@@ -33,7 +33,7 @@ __global__ __launch_bounds__(64 * HNW) void k_head_cdf(HeadCdfArgs a) {
         __syncthreads();
         if (blk + (int)gridDim.x < nblk) head_stage_a(a.A, a.M, a.K, (blk + (int)gridDim.x) * HBM_ROWS, L.As[buf ^ 1]);
         v4i acc[4][CT];
-        head_freqs<CT>(tid, L.As[buf], a.K, a.W, a.V, a.coef, a.total, L, acc);
+        head_freqs<CT, E0>(tid, L.As[buf], a.K, a.W, a.V, a.coef, a.total, L, acc);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int rr = i * 16 + lr;
@@ -99,7 +99,8 @@ bool head_cdf_supported(int V) { return V == 1024; }
 
 void launch_head_cdf(const HeadCdfArgs& a, hipStream_t s) {
     dim3 grid((unsigned)std::min((a.M + HBM_ROWS - 1) / HBM_ROWS, HEAD_GRID));
-    hipLaunchKernelGGL(k_head_cdf<4>, grid, dim3(64 * HNW), 0, s, a);
+    if (a.e0) hipLaunchKernelGGL((k_head_cdf<4, true>), grid, dim3(64 * HNW), 0, s, a);
+    else hipLaunchKernelGGL((k_head_cdf<4, false>), grid, dim3(64 * HNW), 0, s, a);
 }
 
 }  // namespace czip

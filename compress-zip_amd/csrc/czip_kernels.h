@@ -136,6 +136,7 @@ struct HeadCdfArgs {
     int T;
     const uint16_t* lut;       // [256]
     unsigned coef, total;
+    int e0;                    // 1: lut[0] == 65535, so E at table step 0 is the max's E(0) (head_freqs)
     uint32_t* out;             // [., 2]
     long long out_row0;
 };
@@ -222,6 +223,7 @@ struct HeadDecArgs {
     int M, K, V;
     const uint16_t* lut;       // [256]
     unsigned coef, total;
+    int e0;                    // as HeadCdfArgs::e0
     int p;                     // step
 };
 void launch_head_dec(const HeadDecArgs& a, DecState st, DecStreams ds, hipStream_t s);
