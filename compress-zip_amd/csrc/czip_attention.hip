@@ -5,16 +5,20 @@
 namespace czip {
 
 // ---------------------------------------------------------------------------
-// One workgroup = one chunk, one head, 64 query rows: four wavefronts of 16
+// One workgroup = one chunk, one head, 48 query rows: three wavefronts of 16
 // rows that share only the exp table (one barrier, after it is loaded).  Each
 // wave reads its K and V^T operand fragments straight from the caches
 // (16-byte buffer loads; the waves of a workgroup and the workgroups of a
 // chunk read the same tiles, from L1 / L2) and runs attn_tile over its rows;
 // no wave waits for another.
-// LDS: 8.2 KB of table + 4 x 6.5 KB of per-wave buffers, 4 workgroups per CU.
+// LDS: 8.2 KB of table + 3 x 6.5 KB of per-wave buffers, 5 workgroups per CU
+// (15 waves at 128 VGPRs).  Three waves per workgroup measured fastest on the
+// 512-token text chunks: 189 ms per compress step against 206 with two, 210
+// with four, 237 with one and 242-248 with five, six or eight; the order in
+// which a chunk's row blocks are dispatched made no difference.
 // ---------------------------------------------------------------------------
 
-constexpr int ATT_WAVES = 4;  // wavefronts (16 query rows each) per workgroup
+constexpr int ATT_WAVES = 3;  // wavefronts (16 query rows each) per workgroup
 
 template <bool GEN>
 __global__ __launch_bounds__(64 * ATT_WAVES, 4) void k_attention(AttnArgs a) {
