@@ -27,7 +27,7 @@ PEAK_HBM_GBS = 8000.0       # GB/s
 # The commits the two profile-derived constants below were measured at (they go
 # stale when the kernels change; the bench line carries these names with them).
 TRAFFIC_PROFILED_AT = "c4e705c"
-VALU_PROFILED_AT = "1f76ee7"
+VALU_PROFILED_AT = "f9647e6"
 # HBM bytes per token (read + write) of each kernel on the text workload, from
 # two rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0: the factors a
 # plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text.md
@@ -39,7 +39,7 @@ TRAFFIC_WORKLOADS = ("v001_L4_ctx512_text64MiB",)
 # SQ_INSTS_VALU - SQ_INSTS_VALU_MFMA_I8 on the same workload
 # (profiles/counters_compress_v001_ctx512_text8Mtok.md); the VALU issue peak is one wave64
 # instruction per 4 cycles per SIMD: 1024 SIMDs x 2.4 GHz / 4.
-ATTN_VALU_PER_TILE = {"v001_L4_ctx512_text64MiB": 959}
+ATTN_VALU_PER_TILE = {"v001_L4_ctx512_text64MiB": 960}
 PEAK_VALU_GINST = 1024 * 2.4 / 4 * 1e9 / 1e9
 
 WORKLOADS = {
