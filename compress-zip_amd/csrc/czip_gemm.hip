@@ -396,6 +396,17 @@ __device__ __forceinline__ void ws_strip(const GemmArgs& a, const WsOut& ro, con
             mma(i + 1, acc[(i + 1) & 1]);
         }
         epi_ws<EPI, FAST, ROLE>(a, ro, acc[i & 1], r0 + i * 16 + lr, col_base, c4, qr[i & 1], g, t[i]);
+        if (i + 1 < SR / 16) {
+            // the next tile's products between this tile's epilogue VALU, one
+            // MFMA to every three (d512 prefill: up + ReGLU 287 -> 276 ms, QKV
+            // 68 -> 66.5 ms per 16M-token step)
+#pragma unroll
+            for (int n = 0; n < 4 * KS; n++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 }
 
