@@ -546,6 +546,13 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
     }
     __builtin_amdgcn_s_waitcnt(0);  // the block's A (and everything before) has landed
     __syncthreads();
+    if (wave == 0) {
+        // the decoder value (a 64-bit division) while the other waves start
+        // their products, not in the one-wave section after the reductions
+        const unsigned long long range = (unsigned long long)high - low + 1;  // <= 2^32
+        const unsigned long long value = ((unsigned long long)(code - low) + 1) * a.total - 1;
+        row_v[lane] = live ? (unsigned)min(value / range, (unsigned long long)a.total - 1) : 0u;
+    }
     v4i acc[4][CT];
     head_freqs<CT, E0>(tid, L.As[0], a.K, a.W, a.V, a.coef, a.total, L, acc);
     // sum f per row and wave
@@ -573,9 +580,6 @@ __global__ __launch_bounds__(64 * HNW) void k_head_dec(HeadDecArgs a, DecState s
             L.red_c[w][lane] = run;
             run += L.red_b[w][lane] + (w == wam ? rem : 0u);
         }
-        const unsigned long long range = (unsigned long long)high - low + 1;  // <= 2^32
-        const unsigned long long value = ((unsigned long long)(code - low) + 1) * a.total - 1;
-        row_v[lane] = live ? (unsigned)min(value / range, (unsigned long long)a.total - 1) : 0u;
         row_rem[lane] = rem;
     }
     __syncthreads();
