@@ -126,6 +126,45 @@ def test_decode_step_gqa_model(amd, orc, tmp_path):
     assert np.array_equal(got, toks)
 
 
+def _step_case(i: int) -> dict:
+    rng = np.random.default_rng(9100 + i)
+    compat = rng.random() < 0.35
+    if compat:
+        H = int(rng.choice([4, 6, 8]))
+        n_kv = int(rng.integers(1, -(-(64 * H + 256) // 128)))  # one MQA row (attention.rs:176)
+    else:
+        H = int(rng.choice([1, 2, 3, 4, 6, 8, 12, 16]))
+        n_kv = int(rng.choice([g for g in range(1, H + 1) if H % g == 0]))
+    T = int(rng.integers(16, 161))
+    return dict(d=64 * H, n_heads=H, n_kv=n_kv, d_ff=64 * int(rng.integers(1, 33)),
+                vocab=int(rng.choice([1024, 1088, 2048, 8192])), n_layers=int(rng.integers(1, 4)),
+                sink=bool(rng.random() < 0.3), compat=compat, T=T, ctx=T + int(rng.integers(0, 40)),
+                streams=int(rng.integers(3, 25)), tail=int(rng.integers(1, T + 1)), seed=9100 + i)
+
+
+@pytest.mark.parametrize("i", range(8))
+def test_decode_step_random_shapes(amd, orc, tmp_path, i):
+    """Seeded random models (1-16 heads, both KV modes, vocabularies to 8192,
+    sinks) through the step-wise boundary: 3-24 streams, a ragged last one,
+    and the full tables checked against the symbol search every 8 steps."""
+    from czip_amd import synth
+    c = _step_case(i)
+    print(f"decode_step case {i}: {c}", flush=True)
+    path = synth.write_random_model(str(tmp_path / f"s{i}.czm"), d=c["d"], n_layers=c["n_layers"], n_heads=c["n_heads"],
+                                    n_kv=c["n_kv"], d_ff=c["d_ff"], vocab=c["vocab"], ctx=c["ctx"], seed=c["seed"],
+                                    sink=c["sink"])
+    kv = amd.KV_RUST_COMPAT if c["compat"] else amd.KV_GQA
+    gm = amd.Model(amd.ModelWeights(path, kv))
+    om = orc.Model.from_file(path, kv)
+    T, S = c["T"], c["streams"]
+    n = (S - 1) * T + c["tail"]
+    toks = synth.zipf_ids(n, c["vocab"], seed=c["seed"] + 1)
+    chunks = om.compress_many(toks, T, threads=8)
+    ntoks = [min(T, n - T * k) for k in range(len(chunks))]
+    got = _decode_streams(gm, chunks, ntoks, T, gm.target_total, check_tables_every=8)
+    assert np.array_equal(got, toks)
+
+
 def test_decode_step_errors(amd):
     gm = amd.Model(amd.ModelWeights(MODEL_PATH))
     with pytest.raises(amd.CzipError) as e:
