@@ -423,6 +423,14 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
         // weight columns: output lane l holds column l % 16 = the lane's
         // row), less the other streams' columns (KT keys of -32896 each)
         v4i sh = {0, 0, 0, 0}, sl = {0, 0, 0, 0};
+        // from the pass's first products to its end the wave runs at raised
+        // priority: a wave that has formed its weight columns goes ahead of
+        // the waves still forming theirs (or scanning a tile), whose
+        // independent VALU then fills the issue slots its MFMA, LDS and
+        // rescale latencies leave (prefill attention 190.5 -> 184.0 ms per
+        // compress step; from the mask generation on 186.0, only up to the
+        // LDS hand-over 187.2, with the tile's scores raised too 188.6)
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int t = 0; t < NS; t++) {
             sh = Pv::mma(Pv::ONES, bhs[t], sh);
@@ -495,6 +503,7 @@ __device__ __forceinline__ void attn_tile(KOp kop, VOp vop_at, const v4i* qs, in
                     st.vacc[r] = rescale_v(st.vacc[r], (unsigned)__builtin_amdgcn_readlane((int)erow, r)) + bv[r] + corr;
         }
         wave_lds_fence();
+        __builtin_amdgcn_s_setprio(0);
     }
 }
 
