@@ -16,8 +16,9 @@
 // The ReGLU output never reaches HBM; per row the kernel reads the d input
 // bytes and the int16 residual, and writes the residual and the next norm's
 // input.  Weights stream from L2 once per strip per workgroup (the up rows of
-// the next chunk load during the current down phase, the down rows during the
-// up phase, so no extra registers hold them).  The epilogue is the row GEMM's
+// the next chunk load as soon as the last up products have read the current
+// ones, during the last row tile's epilogue and the down phase; the down rows
+// during the up phase; so no extra registers hold them).  The epilogue is the row GEMM's
 // (rn_epilogue in czip_gemm.hip) over R rows.
 #include <algorithm>
 
@@ -156,9 +157,14 @@ __global__ __launch_bounds__(64 * FFN_NW, 1) void k_ffn(FfnArgs a) {
                 ugp = ugn;
                 uup = uun;
             }
+            // the last products have read the chunk's up operands: the next
+            // chunk's (or the next strip's first) load during the last
+            // epilogue (compress step 82.0-82.5 -> 78.4-79.5 ms against
+            // loading them after the barrier)
+            if (c + 1 < NC) load_wu(c + 1);
+            else if (more) load_wu(0);
             up_epi(RT - 1, ugp, uup);
             __syncthreads();  // the chunk's ReGLU bytes are complete
-            if (c + 1 < NC) load_wu(c + 1);
             // down: the chunk's two K steps of 64 features
 #pragma unroll
             for (int k = 0; k < 2; k++)
@@ -231,7 +237,6 @@ __global__ __launch_bounds__(64 * FFN_NW, 1) void k_ffn(FfnArgs a) {
         }
         __syncthreads();
         row_inv();
-        if (more) load_wu(0);
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
             const int row = m0 + rt * 16 + lr;
