@@ -240,6 +240,29 @@ def test_fused_ffn_small_launches(amd, shipped, monkeypatch, chunk, n_chunks):
     assert np.array_equal(gm.decompress_chunks(ref, ntoks), toks)
 
 
+def test_fused_ffn_many_strips(gpu_shipped, shipped):
+    """The default FFN choice at the benchmark's scale: 1,100 chunks of 512
+    (563,183 rows, above the 2^19 rows from which the fused kernel runs):
+    4,400 strips of 128 rows, 17-18 per workgroup, so every workgroup runs
+    the next strip's staged input and up weights requested during the
+    previous strip.  Ten chunks spread over the batch (the first, the
+    ragged last one) against the oracle's bytes, then every chunk decoded
+    on the device."""
+    chunk, n_chunks = 512, 1100
+    rng = np.random.default_rng(1100)
+    n = chunk * n_chunks - 17
+    toks = rng.integers(0, 1024, n).astype(np.uint32)
+    _say(f"compress shipped, fused FFN by default, {n_chunks} x {chunk}")
+    got = gpu_shipped.compress_chunks(toks, chunk)
+    assert len(got) == n_chunks
+    for c in sorted(set(np.linspace(0, n_chunks - 1, 10).astype(int).tolist())):
+        ref = shipped.compress_many(toks[c * chunk:(c + 1) * chunk], chunk, threads=1)
+        assert got[c] == ref[0], f"chunk {c} differs from the oracle"
+    ntoks = [min(chunk, n - chunk * c) for c in range(n_chunks)]
+    _say(f"decompress shipped, {n_chunks} streams")
+    assert np.array_equal(gpu_shipped.decompress_chunks(got, ntoks), toks)
+
+
 def test_requant_general_path(amd, orc, tmp_path):
     """Requantization outside the GEMMs' f64 fast path (|mult| >= 2^26, negative
     multipliers, shift <= 0) against the oracle."""
