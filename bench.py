@@ -27,7 +27,7 @@ PEAK_HBM_GBS = 8000.0       # GB/s
 # The commits the two profile-derived constants below were measured at (they go
 # stale when the kernels change; the bench line carries these names with them).
 TRAFFIC_PROFILED_AT = "c4e705c"
-VALU_PROFILED_AT = "5371079"
+VALU_PROFILED_AT = "493f3e9"
 # HBM bytes per token (read + write) of each kernel on the text workload, from
 # two rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0: the factors a
 # plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text.md
