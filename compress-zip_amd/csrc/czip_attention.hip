@@ -5,30 +5,35 @@
 namespace czip {
 
 // ---------------------------------------------------------------------------
-// One workgroup = one chunk and three wavefronts that share only the exp
-// table (one barrier, after it is loaded): the same 16 query rows of three
-// heads when the head count is a multiple of three (equal tile counts, so no
-// wave of the workgroup idles while another finishes: 181.5-182.3 against
-// 183.4-183.6 ms per compress step of the 6-head shipped model), else 48 rows
-// of one head, 16 per wave.  Each
+// One workgroup = one chunk and NWV wavefronts that share only the exp table
+// (one barrier, after it is loaded).  When the head count allows, the waves
+// take the same 16 query rows of NWV heads: equal tile counts, so no wave of
+// a workgroup idles while another finishes.  Four heads for H a multiple of
+// four: 685-688 against 728-733 ms per compress step for 8 heads at
+// 1024-token chunks (two heads per workgroup: 734-737), 2,252-2,260 against
+// 2,364-2,383 ms for 12 heads at 4096-token chunks (three heads: 2,337-2,348);
+// else three heads for H a multiple of three: 181.5-182.3 against 183.4-183.6
+// ms for the 6-head shipped model (two heads: 186.8; four waves on 64 rows of
+// one head: 202.5-203.6).  Else 48 rows of one head, 16 per wave.  Each
 // wave reads its K and V^T operand fragments straight from the caches
 // (16-byte buffer loads; the waves of a workgroup and the workgroups of a
 // chunk read the same tiles, from L1 / L2) and runs attn_tile over its rows;
 // no wave waits for another.
-// LDS: 8.2 KB of table + 3 x 6.5 KB of per-wave buffers, 5 workgroups per CU
-// (15 waves at 128 VGPRs).  Three waves per workgroup measured fastest on the
-// 512-token text chunks: 189 ms per compress step against 206 with two, 210
-// with four, 237 with one and 242-248 with five, six or eight; the order in
-// which a chunk's row blocks are dispatched made no difference.
+// LDS: 8.2 KB of table + 6.5 KB of per-wave buffers per wave: 5 three-wave
+// or 4 four-wave workgroups per CU (15 or 16 waves at 128 VGPRs).  For rows
+// of one head, three waves per workgroup measured fastest on the 512-token
+// text chunks: 189 ms per compress step against 206 with two, 210 with four,
+// 237 with one and 242-248 with five, six or eight; the order in which a
+// chunk's row blocks are dispatched made no difference.
 // ---------------------------------------------------------------------------
 
-constexpr int ATT_WAVES = 3;  // wavefronts (16 query rows each) per workgroup
-
-template <bool GEN>
-__global__ __launch_bounds__(64 * ATT_WAVES, 4) void k_attention(AttnArgs a) {
-    constexpr int QR = 16 * ATT_WAVES;  // query rows per workgroup
+// NWV wavefronts per workgroup; HWG: the waves take the same 16 rows of NWV
+// heads (H a multiple of NWV), else 16 rows each of one head
+template <bool GEN, int NWV, bool HWG>
+__global__ __launch_bounds__(64 * NWV, 4) void k_attention(AttnArgs a) {
+    constexpr int QR = HWG ? 16 : 16 * NWV;  // query rows per workgroup
     __shared__ __attribute__((aligned(16))) uint16_t etb[ETB_PAD];
-    __shared__ __attribute__((aligned(16))) AttnWaveLds wl[ATT_WAVES];
+    __shared__ __attribute__((aligned(16))) AttnWaveLds wl[NWV];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -36,22 +41,18 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void k_attention(AttnArgs a) {
     // 1-D grid, XCD-aware: workgroups go round-robin over the 8 XCDs; XCD x
     // takes chunks x, x + 8, ..., all (query block, head) pairs of a chunk in a
     // row, so a chunk's K/V tiles are fetched into one L2 only.
-    // H a multiple of the wave count: the waves take the same 16 rows of
-    // ATT_WAVES heads (equal tile counts, the same K/V tiles); else 16 rows
-    // each of one head
-    const bool hwg = a.H % ATT_WAVES == 0;
-    const int nq = hwg ? (a.T + 15) / 16 : (a.T + QR - 1) / QR;
-    const int per_chunk = nq * (hwg ? a.H / ATT_WAVES : a.H);
+    const int nq = (a.T + QR - 1) / QR;
+    const int per_chunk = nq * (HWG ? a.H / NWV : a.H);
     const int xcd = (int)(blockIdx.x % 8u), jx = (int)(blockIdx.x / 8u);
     const int b = (jx / per_chunk) * 8 + xcd;
     if (b >= a.B) return;
-    const int q0 = ((jx % per_chunk) % nq) * (hwg ? 16 : QR);
-    const int h = hwg ? ((jx % per_chunk) / nq) * ATT_WAVES + wave : (jx % per_chunk) / nq;
+    const int q0 = ((jx % per_chunk) % nq) * QR;
+    const int h = HWG ? ((jx % per_chunk) / nq) * NWV + wave : (jx % per_chunk) / nq;
     const int T = a.T, len = a.lens[b];
     if (q0 >= len) return;
-    for (int i = tid; i < ETB_PAD / 8; i += 64 * ATT_WAVES) ((uint4*)etb)[i] = ((const uint4*)a.etab)[i];
+    for (int i = tid; i < ETB_PAD / 8; i += 64 * NWV) ((uint4*)etb)[i] = ((const uint4*)a.etab)[i];
     __syncthreads();
-    const int wrow0 = hwg ? q0 : q0 + wave * 16;
+    const int wrow0 = HWG ? q0 : q0 + wave * 16;
     if (wrow0 >= len) return;  // no barrier follows
     AttnWaveLds& W = wl[wave];
     attn_wave_init(W);
@@ -140,16 +141,26 @@ __global__ __launch_bounds__(64 * ATT_WAVES, 4) void k_attention(AttnArgs a) {
     });
 }
 
+template <bool GEN, int NWV, bool HWG>
+static void launch_attention_t(const AttnArgs& g, int B, hipStream_t s) {
+    constexpr int QR = HWG ? 16 : 16 * NWV;
+    const int nq = (g.T + QR - 1) / QR;
+    dim3 grid((unsigned)(((B + 7) / 8) * 8 * nq * (HWG ? g.H / NWV : g.H)));
+    hipLaunchKernelGGL((k_attention<GEN, NWV, HWG>), grid, dim3(64 * NWV), 0, s, g);
+}
+
+template <bool GEN>
+static void launch_attention_g(const AttnArgs& g, int B, hipStream_t s) {
+    if (g.H % 4 == 0) launch_attention_t<GEN, 4, true>(g, B, s);
+    else if (g.H % 3 == 0) launch_attention_t<GEN, 3, true>(g, B, s);
+    else launch_attention_t<GEN, 3, false>(g, B, s);
+}
+
 void launch_attention(const AttnArgs& a, int B, hipStream_t s) {
     AttnArgs g = a;
     g.B = B;
-    const bool hwg = a.H % ATT_WAVES == 0;
-    dim3 grid((unsigned)(((B + 7) / 8) * 8 *
-                         (hwg ? ((a.T + 15) / 16) * (a.H / ATT_WAVES) : ((a.T + 16 * ATT_WAVES - 1) / (16 * ATT_WAVES)) * a.H)));
-    if (a.general)
-        hipLaunchKernelGGL((k_attention<true>), grid, dim3(64 * ATT_WAVES), 0, s, g);
-    else
-        hipLaunchKernelGGL((k_attention<false>), grid, dim3(64 * ATT_WAVES), 0, s, g);
+    if (a.general) launch_attention_g<true>(g, B, s);
+    else launch_attention_g<false>(g, B, s);
 }
 
 }  // namespace czip
