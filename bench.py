@@ -26,13 +26,13 @@ PEAK_HBM_GBS = 8000.0       # GB/s
 
 # The commits the two profile-derived constants below were measured at (they go
 # stale when the kernels change; the bench line carries these names with them).
-TRAFFIC_PROFILED_AT = "c4e705c"
-VALU_PROFILED_AT = "493f3e9"
+TRAFFIC_PROFILED_AT = "da916f6"
+VALU_PROFILED_AT = "da916f6"
 # HBM bytes per token (read + write) of each kernel on the text workload, from
 # two rocprofv3 --pmc runs (FETCH_SIZE x2.0, WRITE_SIZE x1.0: the factors a
 # plain 256 MiB copy calibrates); profiles/traffic_v001_ctx512_text.md
-TRAFFIC_B_PER_TOKEN = {"attention": 512 + 384, "qkv_table": 12 + 512, "gemm_o_norm": 396 + 1152,
-                       "ffn": 1440 + 384, "gemm_down_norm": 1946 + 384, "gemm_up": 677 + 1024, "head_cdf": 389 + 8}
+TRAFFIC_B_PER_TOKEN = {"attention": 513 + 384, "qkv_table": 12 + 512, "gemm_o_norm": 396 + 1152,
+                       "ffn": 1408 + 386, "gemm_down_norm": 1946 + 384, "gemm_up": 677 + 1024, "head_cdf": 389 + 8}
 TRAFFIC_WORKLOADS = ("v001_L4_ctx512_text64MiB",)
 # Prefill attention: wave64 VALU instructions (MFMA excluded) per 16-row tile (64 keys, or
 # 32 for a row block's last tile when its visible keys end in the first half), from
